@@ -1,0 +1,157 @@
+"""Benchmark of the LEMA hot path on one MI355X; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload zipf_prefill]
+
+zipf_prefill (default): B8 H16 T16384, 24-bit Zipf(1.1) codes over 4096 distinct codes per
+(b, h), d_v 64 bf16. A step is one fused resolve+gather launch over the whole batch, inputs
+resident in HBM: per query it reads the query and key code (4 + 4 B) and a value row
+(128 B, compulsory once) and writes the match index (4 B) and the output row (128 B):
+268 B/query algorithmic, 562 MB per step. `value` = matched queries resolved per second.
+
+`roofline` prices the fused kernel's algorithmic bytes against MI355X's 8 TB/s HBM peak,
+with the kernel time measured by HIP events on the stream it is launched on. `traffic` is
+the HBM bytes per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed in
+profiles/ (null if absent). `cpu_baseline` times the reference's sort-based CPU algorithm
+(torch ops on the host's cores) on a bounded sample of the same workload.
+
+One GPU only: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_QUERY = 4 + 4 + 4 + 128 + 128
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="zipf_prefill", choices=["zipf_prefill"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=16,
+                    help="(b, h) rows of the workload timed for the CPU baseline")
+    return ap.parse_args()
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 PMC counters (profiles/traffic.json)."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(name, {}).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+def cpu_baseline_prefill(qc, kc, v32, rows: int):
+    """The reference's CPU algorithm (attention.py:100-158 via oracle/torch_port.py) on the
+    first `rows` (b, h) rows of the workload, bf16 values, all host cores."""
+    import torch
+    from oracle.torch_port import lema_hard_codes
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    B, H, T = qc.shape
+    q = torch.from_numpy(qc.reshape(B * H, T)[:rows]).view(1, rows, T)
+    k = torch.from_numpy(kc.reshape(B * H, T)[:rows]).view(1, rows, T)
+    v = torch.from_numpy(v32.reshape(B * H, T, -1)[:rows]).to(torch.bfloat16).view(1, rows, T, -1)
+    for _ in range(2):
+        lema_hard_codes(q, k, v)
+    times = []
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 10 and (time.perf_counter() < t_end or len(times) < 3):
+        t0 = time.perf_counter()
+        lema_hard_codes(q, k, v)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": rows * T / med, "unit": "queries/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {B * H} (b,h) rows x T={T} ({rows * T} queries), bf16 "
+                      f"d_v {v.shape[-1]}; median of {len(times)} runs, "
+                      f"{med * 1e3:.1f} ms per run"}
+
+
+def bench_prefill(a):
+    import numpy as np
+    import torch
+    from latest_exact_match_attention_amd import build
+    from latest_exact_match_attention_amd.attention import launch_hard
+    from latest_exact_match_attention_amd.workloads import ZIPF_PREFILL, zipf_prefill
+
+    if not build.LIB.exists():
+        build.build()
+    cfg = ZIPF_PREFILL
+    B, H, T, dv = cfg["B"], cfg["H"], cfg["T"], cfg["dv"]
+    qc, kc, v32 = zipf_prefill(0)
+    dev = torch.device("cuda", 0)
+    qd = torch.from_numpy(qc.reshape(B * H, T)).to(dev).to(torch.int32)
+    kd = torch.from_numpy(kc.reshape(B * H, T)).to(dev).to(torch.int32)
+    vd = torch.from_numpy(v32).to(dev).to(torch.bfloat16)
+    y = torch.empty_like(vd)
+    src = torch.empty((B, H, T), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(a.warmup):
+        launch_hard(qd, kd, vd, y, src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(a.steps):
+        launch_hard(qd, kd, vd, y, src)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / a.steps
+    hits = float((src >= 0).float().mean().item())
+    nq = B * H * T
+    achieved = BYTES_PER_QUERY * nq / (ms * 1e-3) / 1e9
+    cpu = None if a.no_cpu_baseline else cpu_baseline_prefill(qc, kc, v32, a.cpu_rows)
+    return {
+        "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
+        "value": nq / (ms * 1e-3),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32 codes, bf16 values",
+        "data": "synthetic (seeded numpy: Zipf codes, N(0,1) values)",
+        "config": {"workload": "zipf_prefill", "B": B, "H": H, "T": T, "code_bits": cfg["bits"],
+                   "distinct_codes": cfg["distinct"], "zipf_s": cfg["s"], "d_v": dv,
+                   "value_dtype": "bf16", "hit_rate": round(hits, 4),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic("resolve_kernel/zipf_prefill"),
+                     "kernel": "resolve_kernel (fused resolve + gather)",
+                     "bytes_per_query": BYTES_PER_QUERY, "queries_per_launch": nq},
+        "cpu_baseline": cpu,
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got "
+              f"--gpus {a.gpus}", file=sys.stderr)
+        return 2
+    out = bench_prefill(a)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,83 @@
+/* lema_hip.h -- C ABI of liblema_hip.so, the MI355X (gfx950) kernels of Latest Exact Match
+ * Attention's hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers unless stated otherwise; the library never allocates,
+ *     frees or synchronises. Work is enqueued on `stream` (a hipStream_t, NULL = the null
+ *     stream), so every call can be captured into a HIP graph.
+ *   - Sizes and strides are int64 and counted in ELEMENTS of the tensor they describe.
+ *   - Codes are unsigned integers of `code_bytes` bytes (4 or 8). A reference int64 code is the
+ *     same 64-bit pattern (code_bytes = 8); only equality is ever used.
+ *   - Return value: LEMA_OK, or an error status whose message lema_last_error() returns
+ *     (thread-local, valid until the next call on that thread).
+ *
+ * Citations are file:line in moritzbroe/latest_exact_match_attention.
+ */
+#ifndef LEMA_HIP_H
+#define LEMA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum lema_status {
+  LEMA_OK = 0,
+  LEMA_TABLE_FULL = 1, /* the store could not place a key (code/lema/csrc/store.cpp:159-160) */
+  LEMA_BAD_ARG = 2,    /* shapes, strides, alignment or sizes the kernels do not accept */
+  LEMA_HIP_ERROR = 3   /* a HIP runtime call failed (launch, attribute query) */
+};
+
+enum lema_dtype { LEMA_F32 = 0, LEMA_F16 = 1, LEMA_BF16 = 2 };
+
+/* How a query without a match is filled (code/lema/attention.py:157-158 vs store.cpp:92). */
+enum lema_miss { LEMA_MISS_DENSE = 0, /* v[b, h, 0, :] * 0: a signed zero, NaN for inf/NaN */
+                 LEMA_MISS_ZERO = 1 /* +0 bytes, the store path */ };
+
+const char* lema_last_error(void);
+int lema_abi_version(void);
+
+/* Sign-pack projected queries or keys into one code per row.
+ * Replaces pack_codes, code/lema/attention.py:82-97: bit j of the code of row (b, h, t) is
+ * (z[b, h, t, j] >= 0) compared as a float (so -0.0 -> 1, NaN -> 0); LSB = dim 0.
+ *   z      [B, H, T, D] of `dtype`, element strides (z_sb, z_sh, z_st), last dim contiguous
+ *   D      1..64; code_bytes 4 requires D <= 32
+ *   codes  contiguous [B, H, T] of code_bytes                                            */
+int lema_pack_codes(const void* z, int32_t dtype, int64_t B, int64_t H, int64_t T, int32_t D,
+                    int64_t z_sb, int64_t z_sh, int64_t z_st, void* codes, int32_t code_bytes,
+                    void* stream);
+
+/* For each of N rows of T positions: src[n, i] = the largest j < i with
+ * kc[n, j] == qc[n, i], else -1.
+ * Replaces latest_prev_match, code/lema/attention.py:100-132 (the reference returns int64).
+ *   qc, kc  contiguous [N, T] codes of code_bytes
+ *   src     contiguous [N, T] of src_bytes (4 = int32, 8 = int64)                       */
+int lema_latest_prev_match(const void* qc, const void* kc, int32_t code_bytes, int64_t N,
+                           int64_t T, void* src, int32_t src_bytes, void* stream);
+
+/* The exact LEMA op without a store, resolve and gather fused in one kernel:
+ * y[b, h, i, :] = v[b, h, src, :] with src as above, a miss filled per `miss`.
+ * Replaces lema_hard(q, k, v) after pack_codes, code/lema/attention.py:155-158.
+ *   qc, kc  contiguous [B*H, T] codes
+ *   v       [B, H, T, dv] of `dtype`, element strides (v_sb, v_sh, v_st), last dim contiguous
+ *   y       [B, H, T, dv] of `dtype`, element strides (y_sb, y_sh, y_st), last dim contiguous
+ *   src     NULL, or contiguous [B*H, T] of src_bytes receiving the match indices        */
+int lema_hard(const void* qc, const void* kc, int32_t code_bytes, const void* v,
+              int32_t dtype, int64_t B, int64_t H, int64_t T, int64_t dv, int64_t v_sb,
+              int64_t v_sh, int64_t v_st, void* y, int64_t y_sb, int64_t y_sh, int64_t y_st,
+              int32_t miss, void* src, int32_t src_bytes, void* stream);
+
+/* The gather alone, for given indices: y = v[src] (miss per `miss`).
+ * Replaces code/lema/attention.py:157-158. Shapes and strides as in lema_hard;
+ * src is contiguous [B*H, T] of src_bytes, every entry in [-1, T).                      */
+int lema_gather(const void* v, int32_t dtype, int64_t B, int64_t H, int64_t T, int64_t dv,
+                int64_t v_sb, int64_t v_sh, int64_t v_st, const void* src, int32_t src_bytes,
+                void* y, int64_t y_sb, int64_t y_sh, int64_t y_st, int32_t miss,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEMA_HIP_H */

@@ -1,0 +1,80 @@
+"""ctypes binding of liblema_hip.so (the C ABI declared in include/lema_hip.h).
+
+The library is the only compute path: there is no CPU or eager-torch fallback. If it has not
+been built, `lib()` raises and names the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "liblema_hip.so"
+
+OK, TABLE_FULL, BAD_ARG, HIP_ERROR = 0, 1, 2, 3
+F32, F16, BF16 = 0, 1, 2
+MISS_DENSE, MISS_ZERO = 0, 1
+
+DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+FULL_MESSAGE = "hash table full: the store is presized and never grows -- provision more capacity"
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+# name -> argument types, exactly the prototypes of include/lema_hip.h
+PROTOTYPES = {
+    "lema_last_error": ([], ctypes.c_char_p),
+    "lema_abi_version": ([], ctypes.c_int),
+    "lema_pack_codes": ([_p, _i32, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _p, _i32, _p],
+                        ctypes.c_int),
+    "lema_latest_prev_match": ([_p, _p, _i32, _i64, _i64, _p, _i32, _p], ctypes.c_int),
+    "lema_hard": ([_p, _p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64,
+                   _i64, _i64, _i32, _p, _i32, _p], ctypes.c_int),
+    "lema_gather": ([_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i32, _p, _i64,
+                     _i64, _i64, _i32, _p], ctypes.c_int),
+}
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH.name} is not built: the LEMA kernels have no fallback. Build it "
+                f"with `python -m latest_exact_match_attention_amd.build` (hipcc, gfx950).")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in PROTOTYPES.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _LIB = L
+    return _LIB
+
+
+def check(status: int) -> None:
+    """Map a library status to the exception the reference raises for the same failure."""
+    if status == OK:
+        return
+    msg = (lib().lema_last_error() or b"").decode(errors="replace")
+    if status == TABLE_FULL:
+        raise RuntimeError(FULL_MESSAGE)
+    if status == BAD_ARG:
+        raise ValueError(msg)
+    raise RuntimeError(f"HIP error in liblema_hip: {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The raw hipStream_t of the current torch stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise TypeError("liblema_hip runs on HIP devices only: got a tensor on "
+                            f"{t.device}; move the inputs to the GPU")

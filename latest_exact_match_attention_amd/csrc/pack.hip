@@ -1,0 +1,165 @@
+// Sign-packing of projected queries/keys into integer codes (code/lema/attention.py:82-97).
+//
+// Bit j of the code of a row is (z_j >= 0) as a float compare: -0.0 -> 1, NaN -> 0, LSB = dim 0.
+//
+// Dense path (the rows form one packed array in some order of (b, h, t), as for both a
+// contiguous [B, H, T, D] tensor and the transposed [B, T, H, D] projection view): a wavefront
+// takes 64 consecutive rows in MEMORY order, i.e. 64*D consecutive elements. In D steps each
+// lane loads one element (coalesced) and a wavefront ballot turns the 64 sign tests into one
+// 64-bit word of the rows' concatenated bit string; lane l then cuts its row's D bits out of
+// those words (staged in LDS) and writes the code to its (b, h, t) slot.
+// Generic path (any strides, last dim contiguous): one thread per row.
+#include "lema_internal.h"
+
+namespace lema {
+namespace {
+
+template <int DTYPE>
+__device__ __forceinline__ bool nonneg(const void* z, int64_t e) {
+  if constexpr (DTYPE == LEMA_F32) {
+    return static_cast<const float*>(z)[e] >= 0.0f;
+  } else if constexpr (DTYPE == LEMA_BF16) {
+    const uint32_t b = static_cast<uint32_t>(static_cast<const uint16_t*>(z)[e]) << 16;
+    return __uint_as_float(b) >= 0.0f;
+  } else {  // IEEE half, tested on its bits: NaN -> false, -0 -> true
+    const uint32_t h = static_cast<const uint16_t*>(z)[e];
+    if ((h & 0x7C00u) == 0x7C00u && (h & 0x03FFu) != 0) return false;
+    return (h & 0x8000u) == 0 || (h & 0x7FFFu) == 0;
+  }
+}
+
+// Memory order of the rows: m = i0 * E1 * E2 + i1 * E2 + i2, output index sum(i_k * os_k).
+struct DenseArgs {
+  const void* z;
+  void* codes;
+  int64_t R;            // rows
+  int64_t E1, E2;       // extents of the two inner memory-order dims
+  int64_t os0, os1, os2;  // output strides (codes) of the memory-order dims
+  int32_t D;
+};
+
+constexpr int kPackThreads = 256;
+
+template <int DTYPE, typename CodeT>
+__global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
+  __shared__ uint64_t words[kPackThreads / 64][64 + 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * (kPackThreads / 64) + w) * 64;
+  if (m0 >= a.R) return;
+  const int64_t e0 = m0 * a.D, eend = a.R * a.D;
+  for (int it = 0; it < a.D; ++it) {
+    const int64_t e = e0 + static_cast<int64_t>(it) * 64 + lane;
+    const bool bit = e < eend && nonneg<DTYPE>(a.z, e);
+    const uint64_t word = __ballot(bit);
+    if (lane == 0) words[w][it] = word;
+  }
+  if (lane == 0) words[w][a.D] = 0;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int64_t m = m0 + lane;
+  if (m >= a.R) return;
+  const int bitpos = lane * a.D;
+  const int wi = bitpos >> 6, off = bitpos & 63;
+  uint64_t code = words[w][wi] >> off;
+  if (off != 0 && off + a.D > 64) code |= words[w][wi + 1] << (64 - off);
+  if (a.D < 64) code &= (uint64_t(1) << a.D) - 1;
+  const int64_t i2 = m % a.E2;
+  const int64_t r = m / a.E2;
+  const int64_t i1 = r % a.E1, i0 = r / a.E1;
+  static_cast<CodeT*>(a.codes)[i0 * a.os0 + i1 * a.os1 + i2 * a.os2] = static_cast<CodeT>(code);
+}
+
+struct StridedArgs {
+  const void* z;
+  void* codes;
+  int64_t B, H, T;
+  int64_t sb, sh, st;
+  int32_t D;
+};
+
+template <int DTYPE, typename CodeT>
+__global__ __launch_bounds__(kPackThreads) void pack_strided_kernel(StridedArgs a) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kPackThreads + threadIdx.x;
+  if (r >= a.B * a.H * a.T) return;
+  const int64_t t = r % a.T;
+  const int64_t bh = r / a.T;
+  const int64_t h = bh % a.H, b = bh / a.H;
+  const int64_t base = b * a.sb + h * a.sh + t * a.st;
+  uint64_t code = 0;
+  for (int j = 0; j < a.D; ++j)
+    if (nonneg<DTYPE>(a.z, base + j)) code |= uint64_t(1) << j;
+  static_cast<CodeT*>(a.codes)[r] = static_cast<CodeT>(code);
+}
+
+template <typename CodeT>
+int launch_dense(int32_t dtype, const DenseArgs& a, hipStream_t st) {
+  const int64_t grid = (a.R + kPackThreads - 1) / kPackThreads;
+  LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
+  switch (dtype) {
+    case LEMA_F32: pack_dense_kernel<LEMA_F32, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    case LEMA_F16: pack_dense_kernel<LEMA_F16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    default: pack_dense_kernel<LEMA_BF16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+  }
+  return launch_status("pack_dense_kernel");
+}
+
+template <typename CodeT>
+int launch_strided(int32_t dtype, const StridedArgs& a, hipStream_t st) {
+  const int64_t grid = (a.B * a.H * a.T + kPackThreads - 1) / kPackThreads;
+  LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
+  switch (dtype) {
+    case LEMA_F32: pack_strided_kernel<LEMA_F32, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    case LEMA_F16: pack_strided_kernel<LEMA_F16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    default: pack_strided_kernel<LEMA_BF16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+  }
+  return launch_status("pack_strided_kernel");
+}
+
+}  // namespace
+}  // namespace lema
+
+using namespace lema;
+
+extern "C" int lema_pack_codes(const void* z, int32_t dtype, int64_t B, int64_t H, int64_t T,
+                               int32_t D, int64_t z_sb, int64_t z_sh, int64_t z_st, void* codes,
+                               int32_t code_bytes, void* stream) {
+  clear_error();
+  const int es = dtype_size(dtype);
+  LEMA_REQUIRE(es > 0, "unknown value dtype %d", dtype);
+  LEMA_REQUIRE(D >= 1 && D <= 64, "d_qk %d > 64 cannot pack into a uint64", D);
+  LEMA_REQUIRE(code_bytes == 8 || (code_bytes == 4 && D <= 32),
+               "code_bytes %d cannot hold %d-bit codes", code_bytes, D);
+  LEMA_REQUIRE(B >= 0 && H >= 0 && T >= 0, "negative shape");
+  const int64_t R = B * H * T;
+  if (R == 0) return LEMA_OK;
+  LEMA_REQUIRE(z != nullptr && codes != nullptr, "null pointer");
+  LEMA_REQUIRE(aligned(z, es) && aligned(codes, code_bytes), "misaligned pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  // Are the rows one packed array? Drop unit dims, order the rest by stride (outermost
+  // first) and check that each stride is the product of the inner extents times D.
+  struct Dim { int64_t e, s, os; };
+  Dim dims[3] = {{B, z_sb, H * T}, {H, z_sh, T}, {T, z_st, 1}};
+  Dim kept[3];
+  int nk = 0;
+  for (const Dim& d : dims)
+    if (d.e > 1) kept[nk++] = d;
+  for (int i = 0; i < nk; ++i)
+    for (int j = i + 1; j < nk; ++j)
+      if (kept[j].s > kept[i].s) { Dim x = kept[i]; kept[i] = kept[j]; kept[j] = x; }
+  bool dense = true;
+  int64_t need = D;
+  for (int i = nk - 1; i >= 0; --i) {
+    dense = dense && kept[i].s == need;
+    need *= kept[i].e;
+  }
+  if (dense) {
+    Dim full[3] = {{1, 0, 0}, {1, 0, 0}, {1, 0, 0}};
+    for (int i = 0; i < nk; ++i) full[3 - nk + i] = kept[i];
+    DenseArgs a{z, codes, R, full[1].e, full[2].e, full[0].os, full[1].os, full[2].os, D};
+    return code_bytes == 4 ? launch_dense<uint32_t>(dtype, a, st) : launch_dense<uint64_t>(dtype, a, st);
+  }
+  StridedArgs a{z, codes, B, H, T, z_sb, z_sh, z_st, D};
+  return code_bytes == 4 ? launch_strided<uint32_t>(dtype, a, st) : launch_strided<uint64_t>(dtype, a, st);
+}

@@ -1,0 +1,68 @@
+"""The C ABI library without a GPU (CPU only): it loads, exports every entry point the header
+declares, validates arguments on the host with the documented statuses, and the Python API
+refuses CPU tensors instead of falling back to a CPU path."""
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from latest_exact_match_attention_amd import _lib, build
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="module")
+def L():
+    build.ensure_built()
+    return _lib.lib()
+
+
+def _declared():
+    text = (ROOT / "include" / "lema_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(lema_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.PROTOTYPES)
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in _declared():
+        assert hasattr(L, name), name
+    assert L.lema_abi_version() >= 1
+
+
+def test_host_validation_statuses(L):
+    assert L.lema_latest_prev_match(None, None, 3, 1, 1, None, 4, None) == _lib.BAD_ARG
+    assert b"code_bytes" in L.lema_last_error()
+    assert L.lema_pack_codes(None, 2, 1, 1, 1, 65, 0, 0, 0, None, 8, None) == _lib.BAD_ARG
+    assert b"> 64" in L.lema_last_error()
+    assert L.lema_pack_codes(None, 2, 1, 1, 1, 33, 0, 0, 0, None, 4, None) == _lib.BAD_ARG
+    assert L.lema_pack_codes(None, 9, 1, 1, 1, 8, 0, 0, 0, None, 8, None) == _lib.BAD_ARG
+    assert L.lema_hard(None, None, 8, None, 2, -1, 1, 1, 1, 0, 0, 0, None, 0, 0, 0, 0, None, 4,
+                       None) == _lib.BAD_ARG
+    assert L.lema_gather(None, 2, 1, 1, 1, 1, 0, 0, 0, None, 5, None, 0, 0, 0, 0,
+                         None) == _lib.BAD_ARG
+    # empty work is a no-op that touches no pointer
+    assert L.lema_latest_prev_match(None, None, 8, 0, 5, None, 8, None) == _lib.OK
+    assert L.lema_pack_codes(None, 2, 0, 4, 4, 8, 0, 0, 0, None, 8, None) == _lib.OK
+
+
+def test_status_mapping():
+    with pytest.raises(RuntimeError, match="full"):
+        _lib.check(_lib.TABLE_FULL)
+
+
+def test_python_api_refuses_cpu_tensors():
+    from latest_exact_match_attention_amd import latest_prev_match, lema_hard, pack_codes
+    q = torch.randn(1, 2, 8, 4)
+    with pytest.raises(TypeError, match="HIP"):
+        pack_codes(q)
+    with pytest.raises(TypeError, match="HIP"):
+        latest_prev_match(torch.zeros(2, 8, dtype=torch.int64),
+                          torch.zeros(2, 8, dtype=torch.int64))
+    with pytest.raises(TypeError, match="HIP"):
+        lema_hard(q, q, q)
+    with pytest.raises(ValueError, match="> 64"):
+        pack_codes(torch.randn(2, 65))

@@ -1,0 +1,276 @@
+"""Parity of the prefill path on the GPU: pack_codes, latest_prev_match, the fused
+resolve+gather and the standalone gather, against the CPU oracle and the golden fixtures.
+Integer results (codes, indices) and gathered value bits must be identical; NaN payloads
+are compared as NaN (the reference multiplies by the 0/1 mask, which may requiet a NaN).
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from latest_exact_match_attention_amd import (gather_values, latest_prev_match, lema_from_codes,
+                                              lema_hard, pack_codes)
+from latest_exact_match_attention_amd.workloads import dense_plumbing, zipf_prefill
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def to_bf16(a: np.ndarray, dev) -> torch.Tensor:
+    """float32 numpy -> bf16 device tensor (round to nearest even, torch's rule)."""
+    return torch.from_numpy(a).to(dev).to(torch.bfloat16)
+
+
+def same_values(got: np.ndarray, want: np.ndarray, dtype: str) -> bool:
+    """Bitwise equality, except that any NaN equals any NaN."""
+    if dtype == "f32":
+        g, w = got.view(np.uint32), want.view(np.uint32)
+        gn = np.isnan(got.view(np.float32))
+        wn = np.isnan(want.view(np.float32))
+    else:
+        g, w = got.view(np.uint16), want.view(np.uint16)
+        e, m = (0x7F80, 0x7F) if dtype == "bf16" else (0x7C00, 0x3FF)
+        gn = ((g & e) == e) & ((g & m) != 0)
+        wn = ((w & e) == e) & ((w & m) != 0)
+    return bool(np.array_equal(gn, wn) and np.array_equal(g[~gn], w[~wn]))
+
+
+# ------------------------------------------------------------------------ pack codes
+def test_pack_golden(dev):
+    g = np.load(GOLDEN / "pack.npz")
+    for D in (24, 64):
+        z = torch.from_numpy(g[f"z_f32_d{D}"]).to(dev)
+        got = pack_codes(z).cpu().numpy().view(np.uint64)
+        assert np.array_equal(got, g[f"codes_f32_d{D}"]), D
+        for name, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+            z = torch.from_numpy(g[f"z_{name}_d{D}"].view(np.int16)).to(dev).view(dt)
+            got = pack_codes(z).cpu().numpy().view(np.uint64)
+            assert np.array_equal(got, g[f"codes_{name}_d{D}"]), (name, D)
+            if D <= 32:
+                got32 = pack_codes(z, torch.int32).cpu().numpy().view(np.uint32)
+                assert np.array_equal(got32.astype(np.uint64), g[f"codes_{name}_d{D}"])
+
+
+@pytest.mark.parametrize("D", [1, 8, 24, 32, 33, 63, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["contiguous", "projection", "sliced"])
+def test_pack_layouts(dev, D, dtype, layout):
+    B, H, T = 2, 3, 77
+    gen = torch.Generator(device="cpu").manual_seed(D * 7 + H)
+    specials = torch.tensor([0.0, -0.0, float("nan"), float("inf"), -float("inf")]).to(dtype)
+    if layout == "contiguous":
+        base = torch.randn(B, H, T, D, generator=gen).to(dtype)
+        base.view(-1)[:5] = specials
+        z = base
+    elif layout == "projection":          # [B, T, H*D] viewed as [B, H, T, D]
+        base = torch.randn(B, T, H * D, generator=gen).to(dtype)
+        base.view(-1)[:5] = specials
+        z = base.view(B, T, H, D).transpose(1, 2)
+    else:                                 # every other position: not one packed array
+        base = torch.randn(B, H, 2 * T, D, generator=gen).to(dtype)
+        base.view(-1)[:5] = specials
+        z = base[:, :, ::2]
+    zd = base.to(dev)
+    zd = zd if layout == "contiguous" else (
+        zd.view(B, T, H, D).transpose(1, 2) if layout == "projection" else zd[:, :, ::2])
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    zc = z.contiguous()
+    carrier = zc.numpy() if dtype == torch.float32 else zc.view(torch.int16).numpy().view(np.uint16)
+    want = oracle.pack_codes(carrier, name)
+    got = pack_codes(zd).cpu().numpy().view(np.uint64)
+    assert np.array_equal(got, want)
+    if D <= 32:
+        got32 = pack_codes(zd, torch.int32).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got32.astype(np.uint64), want)
+
+
+def test_pack_generic_shape(dev):
+    z = torch.randn(5, 7, 3, 9, 12)
+    got = pack_codes(z.to(dev)).cpu().numpy().view(np.uint64)
+    assert got.shape == (5, 7, 3, 9)
+    assert np.array_equal(got, oracle.pack_codes(z.numpy(), "f32"))
+
+
+# ------------------------------------------------------------------ latest prev match
+def test_latest_match_golden(dev):
+    g = np.load(GOLDEN / "latest_match.npz")
+    qc, kc = torch.from_numpy(g["qc"]).to(dev), torch.from_numpy(g["kc"]).to(dev)
+    assert np.array_equal(latest_prev_match(qc, kc).cpu().numpy(), g["src"])
+    got32 = latest_prev_match(qc, kc, out_dtype=torch.int32).cpu().numpy()
+    assert np.array_equal(got32.astype(np.int64), g["src"])
+
+
+@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 1023, 1024, 1025, 2049, 5000])
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_latest_match_random(dev, T, code_dtype):
+    rng = np.random.default_rng(T)
+    for N, alpha in ((1, 3), (3, 50), (9, 5000)):
+        qc = rng.integers(0, alpha, (N, T))
+        kc = rng.integers(0, alpha, (N, T))
+        want = oracle.latest_prev_match(qc, kc)
+        got = latest_prev_match(torch.from_numpy(qc).to(dev).to(code_dtype),
+                                torch.from_numpy(kc).to(dev).to(code_dtype))
+        assert np.array_equal(got.cpu().numpy(), want), (N, alpha)
+
+
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_latest_match_all_ones_code(dev, code_dtype):
+    """The all-ones pattern is the kernel's empty-slot marker; as a code it must still
+    behave like any other (chunks of 1024 positions, so T = 3000 crosses two boundaries)."""
+    rng = np.random.default_rng(1)
+    T = 3000
+    qc = rng.choice([-1, 0, 1, 7], size=(4, T))
+    kc = rng.choice([-1, 0, 1, 9], size=(4, T))
+    qc[1] = -1
+    kc[1, :] = 5
+    kc[1, 1500] = -1
+    want = oracle.latest_prev_match(qc, kc)
+    got = latest_prev_match(torch.from_numpy(qc).to(dev).to(code_dtype),
+                            torch.from_numpy(kc).to(dev).to(code_dtype)).cpu().numpy()
+    assert np.array_equal(got, want)
+    assert (got[1, 1501:] == 1500).all() and (got[1, :1501] == -1).all()
+
+
+def test_latest_match_structured_rows(dev):
+    T = 4100
+    i = np.arange(T)
+    qc = np.stack([np.full(T, 3), i, i - 3, i // 700, (i * 2654435761) % 4096])
+    kc = np.stack([np.full(T, 3), i, i, i // 700, (i * 2246822519) % 4096])
+    want = oracle.latest_prev_match(qc, kc)
+    got = latest_prev_match(torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev))
+    assert np.array_equal(got.cpu().numpy(), want)
+    assert (want[0] == i - 1).all() and (want[1] == -1).all()
+
+
+def test_empty_and_tiny(dev):
+    e = torch.empty((3, 0), dtype=torch.int64, device=dev)
+    assert latest_prev_match(e, e).shape == (3, 0)
+    one = torch.tensor([[5]], device=dev)
+    assert latest_prev_match(one, one).item() == -1
+    v = torch.randn(1, 1, 1, 8, device=dev)
+    y = lema_from_codes(one.view(1, 1, 1), one.view(1, 1, 1), v)
+    assert (y == 0).all()
+
+
+# ------------------------------------------------------------------- fused + gather
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("miss", ["dense", "zero"])
+def test_gather_golden(dev, dtype, miss):
+    g = np.load(GOLDEN / "gather.npz")
+    src = torch.from_numpy(g["src"]).to(dev)
+    N, T, dv = g["v_f32"].shape
+    if dtype == "f32":
+        v = torch.from_numpy(g["v_f32"]).to(dev)
+    else:
+        v = torch.from_numpy(g["v_bf16"].view(np.int16)).to(dev).view(torch.bfloat16)
+    y = gather_values(v.view(1, N, T, dv), src.view(1, N, T), miss=miss)
+    got = y.cpu().numpy() if dtype == "f32" else bits16(y)
+    want = g[f"y_{dtype}_{miss}"]
+    assert same_values(got.reshape(want.shape), want, dtype)
+    y32 = gather_values(v.view(1, N, T, dv), src.view(1, N, T).to(torch.int32), miss=miss)
+    assert torch.equal(y32.view(torch.uint8), y.view(torch.uint8))
+
+
+def test_dense_plumbing_workload(dev):
+    """B1 H8 T4096, 16-bit codes, fp32 values: indices and outputs bit-exact."""
+    qc, kc, v = dense_plumbing(0)
+    want_src = oracle.latest_prev_match(qc.reshape(8, -1), kc.reshape(8, -1))
+    want_y = oracle.gather(v.reshape(8, 4096, 64), "f32", want_src, 0)
+    for ct in (torch.int64, torch.int32):
+        y, src = lema_from_codes(torch.from_numpy(qc).to(dev).to(ct),
+                                 torch.from_numpy(kc).to(dev).to(ct),
+                                 torch.from_numpy(v).to(dev), return_src=True)
+        assert np.array_equal(src.cpu().numpy().reshape(8, -1), want_src)
+        assert same_values(y.cpu().numpy().reshape(8, 4096, 64), want_y, "f32")
+    assert (want_src >= 0).sum() > 100          # the workload does produce matches
+
+
+def test_zipf_prefill_full_size(dev):
+    """B8 H16 T16384, Zipf 24-bit codes, d_v 64 bf16 -- the benchmark workload at its real
+    size: every index and every output bit against the oracle."""
+    qc, kc, v = zipf_prefill(0)
+    N, T = 128, 16384
+    want_src = oracle.latest_prev_match(qc.reshape(N, T), kc.reshape(N, T))
+    vb = to_bf16(v, dev)
+    y, src = lema_from_codes(torch.from_numpy(qc).to(dev).to(torch.int32),
+                             torch.from_numpy(kc).to(dev).to(torch.int32), vb,
+                             return_src=True)
+    assert np.array_equal(src.cpu().numpy().reshape(N, T), want_src)
+    want_y = oracle.gather(bits16(vb).reshape(N, T, 64), "bf16", want_src, 0)
+    assert same_values(bits16(y).reshape(N, T, 64), want_y, "bf16")
+    hit = (want_src >= 0).mean()
+    assert 0.8 < hit < 0.95          # Zipf(1.1) over 4096 codes: 86.6% of queries match
+
+
+@pytest.mark.parametrize("D", [24, 40])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_lema_hard_end_to_end(dev, D, dtype):
+    """pack -> resolve -> gather from pre-activations laid out like the projections
+    ([B, T, H*D] viewed as [B, H, T, D]); few distinct codes so matches are common."""
+    B, H, T, dv = 2, 4, 1500, 24
+    gen = torch.Generator().manual_seed(D)
+    base = torch.randn(B, T, H, 3, generator=gen)
+    # only 3 free signs per row: ~8 distinct codes per head, many matches
+    zq = base.repeat_interleave(-(-D // 3), dim=-1)[..., :D].reshape(B, T, H * D)
+    zk = torch.roll(base, 5, dims=1).repeat_interleave(-(-D // 3), dim=-1)[..., :D]
+    zk = zk.reshape(B, T, H * D)
+    v = torch.randn(B, T, H * dv, generator=gen)
+    q4 = zq.to(dtype).view(B, T, H, D).transpose(1, 2)
+    k4 = zk.to(dtype).view(B, T, H, D).transpose(1, 2)
+    v4 = v.to(dtype).view(B, T, H, dv).transpose(1, 2)
+    y = lema_hard(q4.to(dev), k4.to(dev), v4.to(dev))
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+
+    def carrier(t):
+        t = t.contiguous()
+        return t.numpy() if dtype == torch.float32 else t.view(torch.int16).numpy().view(np.uint16)
+
+    qc = oracle.pack_codes(carrier(q4), name).reshape(B * H, T)
+    kc = oracle.pack_codes(carrier(k4), name).reshape(B * H, T)
+    src = oracle.latest_prev_match(qc, kc)
+    want = oracle.gather(carrier(v4).reshape(B * H, T, dv), name, src, 0)
+    got = carrier(y.cpu())
+    assert same_values(got.reshape(want.shape), want, name)
+    assert (src >= 0).mean() > 0.5
+
+
+def test_lema_hard_value_gradient(dev):
+    """d/dv of sum(y * w): each source row collects the weights of the queries it serves."""
+    B, H, T, D, dv = 1, 2, 300, 8, 4
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, T, D, generator=gen).sign()
+    q[..., 2:] = 1.0
+    k = torch.roll(q, 1, dims=2)
+    v = torch.randn(B, H, T, dv, generator=gen)
+    w = torch.randn(B, H, T, dv, generator=gen)
+    vd = v.to(dev).requires_grad_(True)
+    y = lema_hard(q.to(dev), k.to(dev), vd)
+    (y * w.to(dev)).sum().backward()
+    qc = oracle.pack_codes(q.numpy(), "f32").reshape(B * H, T)
+    kc = oracle.pack_codes(k.numpy(), "f32").reshape(B * H, T)
+    src = oracle.latest_prev_match(qc, kc)
+    want = np.zeros((B * H, T, dv), dtype=np.float64)
+    for n in range(B * H):
+        for i in range(T):
+            if src[n, i] >= 0:
+                want[n, src[n, i]] += w.numpy().reshape(B * H, T, dv)[n, i]
+    np.testing.assert_allclose(vd.grad.cpu().numpy().reshape(B * H, T, dv), want,
+                               rtol=1e-5, atol=1e-5)
+
+
+def test_runs_on_current_stream(dev):
+    qc, kc, v = dense_plumbing(3, T=2048)
+    s = torch.cuda.Stream()
+    a, b, vv = (torch.from_numpy(x).to(dev) for x in (qc, kc, v))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        y, src = lema_from_codes(a, b, vv, return_src=True)
+    s.synchronize()
+    want = oracle.latest_prev_match(qc.reshape(8, -1), kc.reshape(8, -1))
+    assert np.array_equal(src.cpu().numpy().reshape(8, -1), want)
