@@ -1,22 +1,26 @@
 // The prefill latest-match resolver and the value gather (code/lema/attention.py:100-158).
 //
-// One workgroup owns CHUNK consecutive query positions [c0, c0 + CHUNK) of one (b, h) row,
-// one position per thread. Its answer for query i is the latest key j < i with the same code,
-// found in three places, nearest first:
-//   (a) the same wavefront (64 positions): a 64-step register scan with readlane;
-//   (b) earlier wavefronts of the chunk: for every (sub-block, query code) the chunk offset of
-//       the sub-block's latest such key, turned into an exclusive running max over sub-blocks;
-//   (c) before the chunk: every key in [0, c0) is looked up in an LDS hash table of the
-//       chunk's query codes and raises that code's position with an LDS atomicMax.
-// Only keys whose code some query of the chunk carries matter, so the LDS table has 2*CHUNK
-// slots (load <= 1/2) whatever the code width, and every structure lives in LDS: the kernel
-// needs no scratch memory. Its cost is O(T^2 / CHUNK) table lookups per row for (c), reading
-// the row's key codes from L2; that is cheap next to the gather at the T this path serves
-// (16k: 15 lookups per query), and long rows go through the store instead.
+// One workgroup (256 threads, 4 wavefronts) owns 1024 consecutive query positions
+// [c0, c0 + 1024) of one (b, h) row, four per thread, laid out so that the 64 positions of each
+// "word" (o / 64) are the 64 lanes of one wavefront. Query i's answer, the latest key j < i
+// with the same code, is found nearest first:
+//   (a) earlier lanes of its own word, (b) earlier words of the chunk: every key of the chunk
+//       whose code some query of the chunk carries sets its lane bit in a 64-bit mask kept
+//       per (code, word) in a sparse LDS map, and its word's bit in a per-code word summary;
+//       the answer is then one or two mask lookups and a count-leading-zeros -- O(1) per
+//       query, no per-wavefront scan and no ordering pass;
+//   (c) before the chunk: every key in [0, c0) is looked up in the LDS hash table of the
+//       chunk's query codes and raises that code's latest position with an LDS atomicMax.
+// Both LDS tables are bucketized: 4 slots per bucket, read with one 16-byte LDS load, at
+// load <= 1/2, so a lookup almost always ends after a single read and the wavefront does not
+// wait on its slowest lane's probe chain. The query-code table has 2048 slots for at most
+// 1024 codes whatever the code width, so every structure lives in LDS and the kernel needs
+// no scratch memory. Step (c) costs O(T^2 / 1024) lookups per row, reading the row's key
+// codes from L2 with 16-byte loads one batch ahead; at T = 16k that is 7.5 per query.
 //
-// The gather is fused: after resolving, the workgroup copies its CHUNK value rows
-// v[src] -> y in 16-byte pieces, consecutive threads on consecutive pieces, so both the
-// reads of each source row and the (non-temporal) writes of y are coalesced.
+// The gather is fused: after resolving, the workgroup copies its 1024 value rows
+// v[src] -> y in 16-byte pieces, consecutive threads on consecutive pieces, so both the reads
+// of each source row and the (non-temporal) writes of y are coalesced.
 #include "lema_internal.h"
 
 namespace lema {
@@ -35,33 +39,103 @@ __device__ __forceinline__ uint64_t lds_cas(uint64_t* p, uint64_t cmp, uint64_t 
                    static_cast<unsigned long long>(cmp), static_cast<unsigned long long>(val));
 }
 
-// Fibonacci hashing of the code into [0, 2^LOG).
-template <int LOG, typename CodeT>
-__device__ __forceinline__ int slot_hash(CodeT c) {
-  return static_cast<int>((static_cast<uint64_t>(c) * 0x9E3779B97F4A7C15ull) >> (64 - LOG));
+// 32 bits of a code for hashing (equality always compares the whole code).
+__device__ __forceinline__ uint32_t fold(uint32_t c) { return c; }
+__device__ __forceinline__ uint32_t fold(uint64_t c) {
+  return static_cast<uint32_t>(c) ^ static_cast<uint32_t>(c >> 32);
 }
 
-template <int CHUNK>
-struct Log2 {
-  static constexpr int value = CHUNK <= 1 ? 0 : 1 + Log2<CHUNK / 2>::value;
-};
-template <>
-struct Log2<1> {
-  static constexpr int value = 0;
-};
+// Fibonacci hashing into [0, 2^LOG).
+template <int LOG>
+__device__ __forceinline__ int hash32(uint32_t x) {
+  return static_cast<int>((x * 0x9E3779B1u) >> (32 - LOG));
+}
 
-template <typename CodeT, int CHUNK>
+// Resolver geometry: 256 threads (4 wavefronts) own a chunk of 1024 query positions, 4 per
+// thread. Position o of the chunk is handled by thread o % 256 as its (o / 256)-th position,
+// so the 64 positions of a "word" o / 64 are the 64 lanes of one wavefront.
+constexpr int kThreads = 256;
+constexpr int kPer = 4;
+constexpr int kChunk = kThreads * kPer;
+constexpr int kSlots = 2 * kChunk;  // query-code table: at most kChunk codes, load <= 1/2
+constexpr int kBucketLog = 9;       // 512 buckets of 4 slots
+constexpr int kMapSlots = 2 * kChunk;  // (code slot, word) -> lane mask: at most kChunk keys
+constexpr int kMapBucketLog = 9;
+constexpr uint32_t kMapEmpty = 0xFFFFFFFFu;
+static_assert(kSlots == 4 << kBucketLog && kMapSlots == 4 << kMapBucketLog, "table sizes");
+static_assert(kChunk / 64 <= 32, "word summary is a 32-bit mask");
+
+template <typename CodeT>
 struct ResolveLds {
-  static constexpr int kSlots = 2 * CHUNK;
-  static constexpr int kSub = CHUNK / 64;
-  CodeT code[kSlots + 1];     // slot key, sentinel() = free; [kSlots] stands for the sentinel code
-  int32_t pos[kSlots + 1];    // latest key position before the chunk, -1 = none
-  int16_t id[kSlots + 1];     // dense id (< CHUNK) of an occupied slot
-  int16_t last[kSub][CHUNK];  // [sub-block][id]: chunk offset of the latest key, -1 = none
-  int32_t src[CHUNK];
-  int32_t nid;
+  alignas(16) uint64_t mbits[kMapSlots];  // lanes of that word whose key carries that code
+  alignas(16) CodeT code[kSlots];         // query code of a slot, sentinel() = free
+  alignas(16) uint32_t mkey[kMapSlots];   // code slot << 5 | word, kMapEmpty = free
+  int32_t pos[kSlots + 1];    // latest key position before the chunk, -1 = none; the entry
+  uint32_t summ[kSlots + 1];  // bit w: word w of the chunk holds a key with this code
+                              // [kSlots] of both belongs to the sentinel code itself
   int32_t sent_used;
 };
+
+// The 4 slots of bucket b, one (u32 codes) or two (u64 codes) 16-byte LDS reads.
+template <typename CodeT>
+__device__ __forceinline__ void read_bucket(const CodeT* base, int b, CodeT (&x)[4]) {
+  if constexpr (sizeof(CodeT) == 4) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(base + 4 * b);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  } else {
+    const u32x4 v0 = *reinterpret_cast<const u32x4*>(base + 4 * b);
+    const u32x4 v1 = *reinterpret_cast<const u32x4*>(base + 4 * b + 2);
+    x[0] = (uint64_t(v0.y) << 32) | v0.x; x[1] = (uint64_t(v0.w) << 32) | v0.z;
+    x[2] = (uint64_t(v1.y) << 32) | v1.x; x[3] = (uint64_t(v1.w) << 32) | v1.z;
+  }
+}
+
+// Slot of `key` among the bucket's 4 (first match), or -1; `open` gets whether an empty slot
+// was seen, which ends a probe sequence.
+template <typename KeyT>
+__device__ __forceinline__ int match4(const KeyT (&x)[4], KeyT key, KeyT empty, bool& open) {
+  open = x[0] == empty || x[1] == empty || x[2] == empty || x[3] == empty;
+  return x[0] == key ? 0 : x[1] == key ? 1 : x[2] == key ? 2 : x[3] == key ? 3 : -1;
+}
+
+// Insert `key` into a bucketized table (or find it): returns its slot. The table must have an
+// empty slot somewhere (load <= 1/2 here). Torn 8-byte reads are re-checked atomically.
+template <typename KeyT, int BLOG>
+__device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int b) {
+  for (;;) {
+    KeyT x[4];
+    read_bucket(base, b, x);
+    bool open;
+    const int e = match4(x, key, empty, open);
+    if (e >= 0) {
+      if (sizeof(KeyT) == 4 || lds_cas(&base[4 * b + e], key, key) == key) return 4 * b + e;
+      continue;  // a torn read of a slot being written: read the bucket again
+    }
+    if (!open) {
+      b = (b + 1) & ((1 << BLOG) - 1);
+      continue;
+    }
+    const int f = x[0] == empty ? 0 : x[1] == empty ? 1 : x[2] == empty ? 2 : 3;
+    const KeyT old = lds_cas(&base[4 * b + f], empty, key);
+    if (old == empty || old == key) return 4 * b + f;
+    // another key took that slot first: read the same bucket again
+  }
+}
+
+// Finish a lookup whose first bucket b was read into x: slot of key, or -1 (no concurrent
+// writers: the table is read only after the barrier that ends its construction).
+template <typename KeyT, int BLOG>
+__device__ __forceinline__ int table_find(const KeyT* base, KeyT key, KeyT empty, int b,
+                                          KeyT (&x)[4]) {
+  for (;;) {
+    bool open;
+    const int e = match4(x, key, empty, open);
+    if (e >= 0) return 4 * b + e;
+    if (open) return -1;
+    b = (b + 1) & ((1 << BLOG) - 1);
+    read_bucket(base, b, x);
+  }
+}
 
 // Arguments of the gather half. Strides and row sizes are in BYTES.
 struct GatherArgs {
@@ -81,7 +155,8 @@ struct ResolveArgs {
   const void* kc;
   int64_t N, T;
   int32_t nchunks;
-  void* src;  // optional
+  int32_t kvec;  // key rows allow 16-byte loads of 4 consecutive codes
+  void* src;     // optional
   int32_t src_bytes;
   GatherArgs g;
 };
@@ -155,9 +230,10 @@ struct Piece<2> {
 };
 
 // Copy the value rows of `nrows` consecutive positions starting at c0 of row (b, h): y[c0 + r]
-// = v[src_of(r)]. Thread `t` of `nthreads` takes pieces t, t + nthreads, ... An index outside
-// [0, T) is filled like a miss, so no index can make the kernel read outside v.
-template <int VEC, typename SrcFn>
+// = v[src_of(r)]. Thread `t` of `nthreads` takes pieces t, t + nthreads, ..., with kInFlight
+// independent loads issued before the first store. An index outside [0, T) is filled like a
+// miss, so no index can make the kernel read outside v.
+template <int VEC, int kInFlight, typename SrcFn>
 __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, int64_t c0,
                                             int nrows, int t, int nthreads, SrcFn src_of) {
   typedef Piece<VEC> P;
@@ -165,28 +241,44 @@ __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, in
   const uint8_t* vbase = g.v + b * g.v_sb + h * g.v_sh;
   uint8_t* ybase = g.y + b * g.y_sb + h * g.y_sh + c0 * g.y_st;
   const uint32_t total = static_cast<uint32_t>(nrows) * g.pieces;
-  for (uint32_t idx = t; idx < total; idx += nthreads) {
-    const uint32_t r = g.pdiv.div(idx);
-    const uint32_t pc = idx - r * g.pieces;
-    const int64_t s = src_of(r);
-    typename P::T val;
-    if (s >= 0 && s < g.T) {
-      val = P::load(vbase + s * g.v_st + pc * VEC);
-    } else if (g.miss == LEMA_MISS_ZERO) {
-      val = P::zero();
-    } else {
-      val = P::miss(P::load(vbase + pc * VEC), g.dtype);
+  for (uint32_t base = t; base < total; base += kInFlight * nthreads) {
+    typename P::T val[kInFlight];
+    const uint8_t* from[kInFlight];
+    uint8_t* to[kInFlight];
+    int kind[kInFlight];  // 0 none, 1 copy, 2 miss from v[0], 3 zero
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      const uint32_t idx = base + u * nthreads;
+      kind[u] = 0;
+      if (idx >= total) continue;
+      const uint32_t r = g.pdiv.div(idx);
+      const uint32_t pc = idx - r * g.pieces;
+      const int64_t s = src_of(r);
+      to[u] = ybase + static_cast<int64_t>(r) * g.y_st + pc * VEC;
+      if (s >= 0 && s < g.T) {
+        kind[u] = 1;
+        from[u] = vbase + s * g.v_st + pc * VEC;
+      } else {
+        kind[u] = g.miss == LEMA_MISS_ZERO ? 3 : 2;
+        from[u] = vbase + pc * VEC;
+      }
     }
-    P::store(ybase + static_cast<int64_t>(r) * g.y_st + pc * VEC, val);
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u)
+      if (kind[u] == 1 || kind[u] == 2) val[u] = P::load(from[u]);
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      if (kind[u] == 0) continue;
+      const typename P::T out =
+          kind[u] == 1 ? val[u] : (kind[u] == 2 ? P::miss(val[u], g.dtype) : P::zero());
+      P::store(to[u], out);
+    }
   }
 }
 
-template <typename CodeT, int CHUNK, int VEC>
-__global__ __launch_bounds__(CHUNK) void resolve_kernel(ResolveArgs a) {
-  typedef ResolveLds<CodeT, CHUNK> L;
-  constexpr int kSlots = L::kSlots, kMask = kSlots - 1, kSub = L::kSub;
-  constexpr int kLog = Log2<kSlots>::value;
-  __shared__ L s;
+template <typename CodeT, int VEC>
+__global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
+  __shared__ ResolveLds<CodeT> s;
 
   // XCD-aware work mapping: every chunk of row r runs on XCD r % 8, which then keeps that
   // row's key codes and value rows in its own L2; the heaviest chunks (latest) go first.
@@ -197,133 +289,179 @@ __global__ __launch_bounds__(CHUNK) void resolve_kernel(ResolveArgs a) {
   const int64_t row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
   if (row >= a.N) return;
 
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
   const CodeT SENT = sentinel<CodeT>();
   const CodeT* qrow = static_cast<const CodeT*>(a.qc) + row * a.T;
   const CodeT* krow = static_cast<const CodeT*>(a.kc) + row * a.T;
-  const int64_t c0 = static_cast<int64_t>(chunk) * CHUNK;
-  const int64_t i = c0 + t;
-  const bool active = i < a.T;
-  const CodeT q = active ? qrow[i] : CodeT(0);
-  const CodeT kk = active ? krow[i] : CodeT(0);
+  const int32_t c0 = chunk * kChunk;
+  const int n_here = static_cast<int>(a.T - c0 < kChunk ? a.T - c0 : kChunk);
 
-  for (int x = t; x <= kSlots; x += CHUNK) {
-    s.code[x] = SENT;
-    s.pos[x] = -1;
+  CodeT q[kPer], kk[kPer];
+#pragma unroll
+  for (int p = 0; p < kPer; ++p) {
+    const int o = p * kThreads + t;
+    q[p] = o < n_here ? qrow[c0 + o] : CodeT(0);
+    kk[p] = o < n_here ? krow[c0 + o] : CodeT(0);
   }
-  {
-    uint32_t* lw = reinterpret_cast<uint32_t*>(&s.last[0][0]);
-    for (int x = t; x < kSub * CHUNK / 2; x += CHUNK) lw[x] = 0xFFFFFFFFu;
-  }
-  if (t == 0) {
-    s.nid = 0;
-    s.sent_used = 0;
-  }
-  __syncthreads();
-
-  // 1. the chunk's query codes -> slots; the first claimant of a slot gives it a dense id
-  int qs = kSlots;
-  if (active) {
-    if (q == SENT) {
-      if (atomicCAS(&s.sent_used, 0, 1) == 0) s.id[kSlots] = static_cast<int16_t>(atomicAdd(&s.nid, 1));
-    } else {
-      int h = slot_hash<kLog>(q);
-      for (;;) {
-        const CodeT old = lds_cas(&s.code[h], SENT, q);
-        if (old == SENT) {
-          s.id[h] = static_cast<int16_t>(atomicAdd(&s.nid, 1));
-          break;
-        }
-        if (old == q) break;
-        h = (h + 1) & kMask;
+  // Keys before the chunk stream in batches of 1024 (4 per thread), the next batch loaded
+  // while the current one is looked up; c0 is a multiple of the batch.
+  constexpr int kBatch = 4 * kThreads;
+  CodeT nxt[4];
+  auto load_batch = [&](int32_t j0) {
+    if (a.kvec) {  // 4 consecutive codes per thread, 16-byte aligned
+      const CodeT* p = krow + j0 + 4 * t;
+      if constexpr (sizeof(CodeT) == 4) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+        nxt[0] = v.x; nxt[1] = v.y; nxt[2] = v.z; nxt[3] = v.w;
+      } else {
+        const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 2);
+        nxt[0] = (uint64_t(v0.y) << 32) | v0.x; nxt[1] = (uint64_t(v0.w) << 32) | v0.z;
+        nxt[2] = (uint64_t(v1.y) << 32) | v1.x; nxt[3] = (uint64_t(v1.w) << 32) | v1.z;
       }
-      qs = h;
-    }
-  }
-  __syncthreads();
-
-  // the slot of code c among the chunk's query codes, or -1
-  auto find = [&](CodeT c) -> int {
-    if (c == SENT) return s.sent_used ? kSlots : -1;
-    int h = slot_hash<kLog>(c);
-    for (;;) {
-      const CodeT x = s.code[h];
-      if (x == c) return h;
-      if (x == SENT) return -1;
-      h = (h + 1) & kMask;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) nxt[e] = krow[j0 + e * kThreads + t];
     }
   };
+  if (c0 > 0) load_batch(0);
 
-  // 2. (c) keys before the chunk raise their code's latest position
-  for (int64_t j0 = 0; j0 < c0; j0 += 4 * CHUNK) {
-    CodeT kj[4];
+  for (int x = t; x < kSlots; x += kThreads) s.code[x] = SENT;
+  for (int x = t; x <= kSlots; x += kThreads) {
+    s.pos[x] = -1;
+    s.summ[x] = 0;
+  }
+  for (int x = t; x < kMapSlots; x += kThreads) {
+    s.mkey[x] = kMapEmpty;
+    s.mbits[x] = 0;
+  }
+  if (t == 0) s.sent_used = 0;
+  __syncthreads();
+
+  // 1. the chunk's query codes -> table slots; the sentinel code has its own slot kSlots
+  int qs[kPer];
+#pragma unroll
+  for (int p = 0; p < kPer; ++p) {
+    qs[p] = kSlots;
+    if (p * kThreads + t >= n_here) continue;
+    if (q[p] == SENT) {
+      s.sent_used = 1;
+      continue;
+    }
+    qs[p] = table_claim<CodeT, kBucketLog>(s.code, q[p], SENT, hash32<kBucketLog>(fold(q[p])));
+  }
+  __syncthreads();
+
+  const bool sent_used = s.sent_used != 0;
+  // slot of key code c (first bucket b already read into x) among the query codes, or -1
+  auto find_code = [&](CodeT c, int b, CodeT (&x)[4]) -> int {
+    if (c == SENT) return sent_used ? kSlots : -1;
+    return table_find<CodeT, kBucketLog>(s.code, c, SENT, b, x);
+  };
+
+  // 2a. keys inside the chunk: each sets its lane in its (code, word) mask
+  {
+    int b[kPer];
+    CodeT x[kPer][4];
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {  // first bucket reads of all 4 positions together
+      b[p] = hash32<kBucketLog>(fold(kk[p]));
+      read_bucket(s.code, b[p], x[p]);
+    }
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int o = p * kThreads + t;
+      if (o >= n_here) continue;
+      const int sl = find_code(kk[p], b[p], x[p]);
+      if (sl < 0) continue;
+      const int wd = o >> 6;
+      const uint32_t key = (static_cast<uint32_t>(sl) << 5) | wd;
+      const int m = table_claim<uint32_t, kMapBucketLog>(s.mkey, key, kMapEmpty,
+                                                         hash32<kMapBucketLog>(key));
+      atomicOr(reinterpret_cast<unsigned long long*>(&s.mbits[m]), 1ull << lane);
+      atomicOr(&s.summ[sl], 1u << wd);
+    }
+  }
+  // 2b. keys before the chunk raise their code's latest position
+  for (int32_t j0 = 0; j0 < c0; j0 += kBatch) {
+    CodeT cur[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cur[e] = nxt[e];
+    if (j0 + kBatch < c0) load_batch(j0 + kBatch);
+    int b[4];
+    CodeT x[4][4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int64_t j = j0 + e * CHUNK + t;
-      kj[e] = j < c0 ? krow[j] : CodeT(0);
+      b[e] = hash32<kBucketLog>(fold(cur[e]));
+      read_bucket(s.code, b[e], x[e]);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int64_t j = j0 + e * CHUNK + t;
-      if (j < c0) {
-        const int sl = find(kj[e]);
-        if (sl >= 0) atomicMax(&s.pos[sl], static_cast<int32_t>(j));
+      const int sl = find_code(cur[e], b[e], x[e]);
+      if (sl >= 0) atomicMax(&s.pos[sl], a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t);
+    }
+  }
+  __syncthreads();
+
+  // 3. resolve: the latest earlier lane of the own word, else the latest earlier word of the
+  // chunk holding the code, else the latest position before the chunk
+  int32_t src[kPer];
+  {
+    int mb[kPer];
+    uint32_t mx[kPer][4], key0[kPer];
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {  // first map reads of every position's own (code, word)
+      key0[p] = (static_cast<uint32_t>(qs[p]) << 5) | ((p * kThreads + t) >> 6);
+      mb[p] = hash32<kMapBucketLog>(key0[p]);
+      read_bucket(s.mkey, mb[p], mx[p]);
+    }
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int o = p * kThreads + t;
+      src[p] = -1;
+      if (o >= n_here) continue;
+      const uint32_t sl = static_cast<uint32_t>(qs[p]);
+      const int wd = o >> 6;
+      const int m = table_find<uint32_t, kMapBucketLog>(s.mkey, key0[p], kMapEmpty, mb[p], mx[p]);
+      const uint64_t below = m >= 0 ? (s.mbits[m] & ((1ull << lane) - 1)) : 0;
+      if (below) {
+        src[p] = c0 + (wd << 6) + 63 - __clzll(below);
+        continue;
+      }
+      const uint32_t words = s.summ[sl] & ((1u << wd) - 1);
+      if (words) {
+        const int w2 = 31 - __clz(words);
+        const uint32_t key2 = (sl << 5) | w2;
+        uint32_t y2[4];
+        const int b2 = hash32<kMapBucketLog>(key2);
+        read_bucket(s.mkey, b2, y2);
+        const int m2 = table_find<uint32_t, kMapBucketLog>(s.mkey, key2, kMapEmpty, b2, y2);
+        src[p] = c0 + (w2 << 6) + 63 - __clzll(s.mbits[m2]);
+      } else {
+        src[p] = s.pos[sl];
       }
     }
   }
-
-  // 3. (a) + (b) keys inside the chunk
-  int kid = -1;
-  if (active) {
-    const int sl = find(kk);
-    if (sl >= 0) kid = s.id[sl];
-  }
-  const int qid = active ? static_cast<int>(s.id[qs]) : -2;
-  int qbest = -1;
-  bool klast = true;
+  if (a.src != nullptr) {
 #pragma unroll
-  for (int l2 = 0; l2 < 64; ++l2) {
-    const int o = __builtin_amdgcn_readlane(kid, l2);
-    if (o == qid && l2 < lane) qbest = l2;
-    if (o == kid && l2 > lane) klast = false;
-  }
-  if (kid >= 0 && klast) s.last[w][kid] = static_cast<int16_t>(t);
-  __syncthreads();
-
-  const int nid = s.nid;
-  for (int x = t; x < nid; x += CHUNK) {
-    int run = -1;
-#pragma unroll
-    for (int ww = 0; ww < kSub; ++ww) {
-      const int m = s.last[ww][x];
-      s.last[ww][x] = static_cast<int16_t>(run);
-      run = m > run ? m : run;
-    }
-  }
-  __syncthreads();
-
-  int32_t src = -1;
-  if (active) {
-    if (qbest >= 0) {
-      src = static_cast<int32_t>(c0 + w * 64 + qbest);
-    } else {
-      const int m = s.last[w][qid];
-      src = m >= 0 ? static_cast<int32_t>(c0 + m) : s.pos[qs];
-    }
-    if (a.src != nullptr) {
+    for (int p = 0; p < kPer; ++p) {
+      const int o = p * kThreads + t;
+      if (o >= n_here) continue;
       if (a.src_bytes == 8)
-        static_cast<int64_t*>(a.src)[row * a.T + i] = src;
+        static_cast<int64_t*>(a.src)[row * a.T + c0 + o] = src[p];
       else
-        static_cast<int32_t*>(a.src)[row * a.T + i] = src;
+        static_cast<int32_t*>(a.src)[row * a.T + c0 + o] = src[p];
     }
   }
 
   if constexpr (VEC > 0) {
-    s.src[t] = src;
+    int32_t* srcs = reinterpret_cast<int32_t*>(s.mbits);  // the masks are dead now
     __syncthreads();
-    const int nrows = static_cast<int>(a.T - c0 < CHUNK ? a.T - c0 : CHUNK);
-    gather_rows<VEC>(a.g, row, c0, nrows, t, CHUNK,
-                     [&](uint32_t r) -> int64_t { return s.src[r]; });
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) srcs[p * kThreads + t] = src[p];
+    __syncthreads();
+    gather_rows<VEC, 8>(a.g, row, c0, n_here, t, kThreads,
+                        [&](uint32_t r) -> int64_t { return srcs[r]; });
   }
 }
 
@@ -355,11 +493,9 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherOnlyArgs a) {
                                : static_cast<const int32_t*>(a.src)[at];
   }
   __syncthreads();
-  gather_rows<VEC>(a.g, row, c0, nrows, threadIdx.x, blockDim.x,
-                   [&](uint32_t r) -> int64_t { return ssrc[r]; });
+  gather_rows<VEC, 8>(a.g, row, c0, nrows, threadIdx.x, blockDim.x,
+                      [&](uint32_t r) -> int64_t { return ssrc[r]; });
 }
-
-constexpr int kChunk = 1024;
 
 // Largest piece size that divides every byte offset the gather forms.
 int piece_bytes(int64_t row_bytes, const void* v, const void* y,
@@ -407,12 +543,13 @@ int launch_resolve(ResolveArgs& a, int vec, hipStream_t st) {
   const int64_t groups = (a.N + kNumXcd - 1) / kNumXcd;
   const int64_t grid = groups * kNumXcd * a.nchunks;
   LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows x chunks (%lld)", (long long)grid);
+  a.kvec = (aligned(a.kc, 16) && (a.T * static_cast<int64_t>(sizeof(CodeT))) % 16 == 0) ? 1 : 0;
   switch (vec) {
-    case 0: resolve_kernel<CodeT, kChunk, 0><<<dim3(grid), dim3(kChunk), 0, st>>>(a); break;
-    case 16: resolve_kernel<CodeT, kChunk, 16><<<dim3(grid), dim3(kChunk), 0, st>>>(a); break;
-    case 8: resolve_kernel<CodeT, kChunk, 8><<<dim3(grid), dim3(kChunk), 0, st>>>(a); break;
-    case 4: resolve_kernel<CodeT, kChunk, 4><<<dim3(grid), dim3(kChunk), 0, st>>>(a); break;
-    case 2: resolve_kernel<CodeT, kChunk, 2><<<dim3(grid), dim3(kChunk), 0, st>>>(a); break;
+    case 0: resolve_kernel<CodeT, 0><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 16: resolve_kernel<CodeT, 16><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 8: resolve_kernel<CodeT, 8><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 4: resolve_kernel<CodeT, 4><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 2: resolve_kernel<CodeT, 2><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
     default: set_error("internal: piece size %d", vec); return LEMA_BAD_ARG;
   }
   return launch_status("resolve_kernel");
@@ -421,7 +558,7 @@ int launch_resolve(ResolveArgs& a, int vec, hipStream_t st) {
 int check_rows(const void* qc, const void* kc, int32_t code_bytes, int64_t N, int64_t T) {
   LEMA_REQUIRE(code_bytes == 4 || code_bytes == 8, "code_bytes must be 4 or 8, got %d", code_bytes);
   LEMA_REQUIRE(N >= 0 && T >= 0, "negative shape N=%lld T=%lld", (long long)N, (long long)T);
-  LEMA_REQUIRE(T < (int64_t(1) << 31), "T=%lld exceeds int32 positions", (long long)T);
+  LEMA_REQUIRE(T < (int64_t(1) << 30), "T=%lld exceeds the resolver's positions", (long long)T);
   LEMA_REQUIRE(N * T == 0 || (qc != nullptr && kc != nullptr), "null code pointer");
   LEMA_REQUIRE(N * T == 0 || (aligned(qc, code_bytes) && aligned(kc, code_bytes)),
                "code pointers must be aligned to code_bytes");
