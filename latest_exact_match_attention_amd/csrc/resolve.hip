@@ -45,10 +45,10 @@ __device__ __forceinline__ uint32_t fold(uint64_t c) {
   return static_cast<uint32_t>(c) ^ static_cast<uint32_t>(c >> 32);
 }
 
-// Fibonacci hashing into [0, 2^LOG).
-template <int LOG>
-__device__ __forceinline__ int hash32(uint32_t x) {
-  return static_cast<int>((x * 0x9E3779B1u) >> (32 - LOG));
+// Fibonacci hashing, then Lemire's fastrange into [0, n) (n need not be a power of two).
+template <int N>
+__device__ __forceinline__ int bucket_of(uint32_t x) {
+  return static_cast<int>(__umulhi(x * 0x9E3779B1u, static_cast<uint32_t>(N)));
 }
 
 // Resolver geometry: 256 threads (4 wavefronts) own a chunk of 1024 query positions, 4 per
@@ -58,21 +58,21 @@ constexpr int kThreads = 256;
 constexpr int kPer = 4;
 constexpr int kChunk = kThreads * kPer;
 constexpr int kSlots = 2 * kChunk;  // query-code table: at most kChunk codes, load <= 1/2
-constexpr int kBucketLog = 9;       // 512 buckets of 4 slots
-constexpr int kMapSlots = 2 * kChunk;  // (code slot, word) -> lane mask: at most kChunk keys
-constexpr int kMapBucketLog = 9;
+constexpr int kBuckets = kSlots / 4;
+constexpr int kMapSlots = 3 * kChunk / 2;  // (code slot, word) -> lane mask: at most kChunk
+constexpr int kMapBuckets = kMapSlots / 4;  // keys, load <= 2/3
 constexpr uint32_t kMapEmpty = 0xFFFFFFFFu;
-static_assert(kSlots == 4 << kBucketLog && kMapSlots == 4 << kMapBucketLog, "table sizes");
-static_assert(kChunk / 64 <= 32, "word summary is a 32-bit mask");
+static_assert(kChunk / 64 <= 16, "word summary is a 16-bit mask");
 
 template <typename CodeT>
 struct ResolveLds {
   alignas(16) uint64_t mbits[kMapSlots];  // lanes of that word whose key carries that code
   alignas(16) CodeT code[kSlots];         // query code of a slot, sentinel() = free
-  alignas(16) uint32_t mkey[kMapSlots];   // code slot << 5 | word, kMapEmpty = free
+  alignas(16) uint32_t mkey[kMapSlots];   // code slot << 4 | word, kMapEmpty = free
   int32_t pos[kSlots + 1];    // latest key position before the chunk, -1 = none; the entry
-  uint32_t summ[kSlots + 1];  // bit w: word w of the chunk holds a key with this code
-                              // [kSlots] of both belongs to the sentinel code itself
+                              // [kSlots] here and in summ belongs to the sentinel code itself
+  alignas(4) uint16_t summ[kSlots + 2];  // bit w: word w of the chunk holds a key with this
+                                         // code; updated as 32-bit pairs
   int32_t sent_used;
 };
 
@@ -98,10 +98,13 @@ __device__ __forceinline__ int match4(const KeyT (&x)[4], KeyT key, KeyT empty, 
   return x[0] == key ? 0 : x[1] == key ? 1 : x[2] == key ? 2 : x[3] == key ? 3 : -1;
 }
 
-// Insert `key` into a bucketized table (or find it): returns its slot. The table must have an
-// empty slot somewhere (load <= 1/2 here). Torn 8-byte reads are re-checked atomically.
-template <typename KeyT, int BLOG>
-__device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int b) {
+// Insert `key` into a table of NB buckets (or find it): returns its slot; `inserted` tells
+// whether this call put it there. The table must have an empty slot somewhere (load < 1
+// here). Torn 8-byte reads are re-checked atomically.
+template <typename KeyT, int NB>
+__device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int b,
+                                           bool& inserted) {
+  inserted = false;
   for (;;) {
     KeyT x[4];
     read_bucket(base, b, x);
@@ -112,11 +115,12 @@ __device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int
       continue;  // a torn read of a slot being written: read the bucket again
     }
     if (!open) {
-      b = (b + 1) & ((1 << BLOG) - 1);
+      b = b + 1 == NB ? 0 : b + 1;
       continue;
     }
     const int f = x[0] == empty ? 0 : x[1] == empty ? 1 : x[2] == empty ? 2 : 3;
     const KeyT old = lds_cas(&base[4 * b + f], empty, key);
+    if (old == empty) inserted = true;
     if (old == empty || old == key) return 4 * b + f;
     // another key took that slot first: read the same bucket again
   }
@@ -124,7 +128,7 @@ __device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int
 
 // Finish a lookup whose first bucket b was read into x: slot of key, or -1 (no concurrent
 // writers: the table is read only after the barrier that ends its construction).
-template <typename KeyT, int BLOG>
+template <typename KeyT, int NB>
 __device__ __forceinline__ int table_find(const KeyT* base, KeyT key, KeyT empty, int b,
                                           KeyT (&x)[4]) {
   for (;;) {
@@ -132,7 +136,7 @@ __device__ __forceinline__ int table_find(const KeyT* base, KeyT key, KeyT empty
     const int e = match4(x, key, empty, open);
     if (e >= 0) return 4 * b + e;
     if (open) return -1;
-    b = (b + 1) & ((1 << BLOG) - 1);
+    b = b + 1 == NB ? 0 : b + 1;
     read_bucket(base, b, x);
   }
 }
@@ -146,6 +150,7 @@ struct GatherArgs {
   int64_t y_sb, y_sh, y_st;
   uint32_t pieces;  // 16/8/4/2-byte pieces per value row
   FastDiv pdiv;     // division by `pieces`
+  int32_t plog;     // log2(pieces) when pieces is a power of two <= 64, else -1
   int32_t miss;
   int32_t dtype;
 };
@@ -233,13 +238,46 @@ struct Piece<2> {
 // = v[src_of(r)]. Thread `t` of `nthreads` takes pieces t, t + nthreads, ..., with kInFlight
 // independent loads issued before the first store. An index outside [0, T) is filled like a
 // miss, so no index can make the kernel read outside v.
-template <int VEC, int kInFlight, typename SrcFn>
+template <int VEC, int kInFlight, int kInFlightP2, typename SrcFn>
 __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, int64_t c0,
                                             int nrows, int t, int nthreads, SrcFn src_of) {
   typedef Piece<VEC> P;
   const int64_t b = row / g.H, h = row - (row / g.H) * g.H;
   const uint8_t* vbase = g.v + b * g.v_sb + h * g.v_sh;
   uint8_t* ybase = g.y + b * g.y_sb + h * g.y_sh + c0 * g.y_st;
+  if (g.plog >= 0) {
+    // pieces = 2^plog divides the block: thread t always copies piece t % pieces of rows
+    // t / pieces + k * (nthreads / pieces), with kInFlight of them loaded before storing
+    const int rpp = nthreads >> g.plog;
+    const int r0 = t >> g.plog, pc = t & ((1 << g.plog) - 1);
+    const uint8_t* vp = vbase + pc * VEC;
+    uint8_t* yp = ybase + pc * VEC;
+    for (int rb = r0; rb < nrows; rb += kInFlightP2 * rpp) {
+      typename P::T val[kInFlightP2];
+      int32_t sv[kInFlightP2];
+#pragma unroll
+      for (int u = 0; u < kInFlightP2; ++u) {
+        const int r = rb + u * rpp;
+        const int64_t x = r < nrows ? src_of(r) : -2;
+        sv[u] = r >= nrows ? -2 : (x >= 0 && x < g.T ? static_cast<int32_t>(x) : -1);
+      }
+#pragma unroll
+      for (int u = 0; u < kInFlightP2; ++u) {
+        if (sv[u] >= 0)
+          val[u] = P::load(vp + sv[u] * g.v_st);
+        else if (sv[u] == -1 && g.miss != LEMA_MISS_ZERO)
+          val[u] = P::load(vp);
+      }
+#pragma unroll
+      for (int u = 0; u < kInFlightP2; ++u) {
+        if (sv[u] == -2) continue;
+        const typename P::T out = sv[u] >= 0 ? val[u]
+                                  : (g.miss == LEMA_MISS_ZERO ? P::zero() : P::miss(val[u], g.dtype));
+        P::store(yp + static_cast<int64_t>(rb + u * rpp) * g.y_st, out);
+      }
+    }
+    return;
+  }
   const uint32_t total = static_cast<uint32_t>(nrows) * g.pieces;
   for (uint32_t base = t; base < total; base += kInFlight * nthreads) {
     typename P::T val[kInFlight];
@@ -276,20 +314,30 @@ __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, in
   }
 }
 
-template <typename CodeT, int VEC>
-__global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
-  __shared__ ResolveLds<CodeT> s;
+// Find 4 keys at once (first bucket reads issued together); -1 where absent or inactive.
+template <typename KeyT, int NB>
+__device__ __forceinline__ void find4(const KeyT* base, const KeyT (&key)[4], KeyT empty,
+                                      int (&slot)[4]) {
+  int b[4];
+  KeyT x[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    b[i] = bucket_of<NB>(fold(key[i]));
+    read_bucket(base, b[i], x[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) slot[i] = table_find<KeyT, NB>(base, key[i], empty, b[i], x[i]);
+}
 
-  // XCD-aware work mapping: every chunk of row r runs on XCD r % 8, which then keeps that
-  // row's key codes and value rows in its own L2; the heaviest chunks (latest) go first.
-  const int bid = blockIdx.x;
-  const int xcd = bid % kNumXcd;
-  const int k = bid / kNumXcd;
-  const int chunk = a.nchunks - 1 - (k % a.nchunks);
-  const int64_t row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
-  if (row >= a.N) return;
-
-  const int t = threadIdx.x, lane = t & 63;
+// Resolve the 1024 queries of chunk `chunk` of row `row` with the 256 threads t = 0..255
+// (four wavefronts), synchronising them with `bar`; leaves each thread's answers in src[p]
+// for positions p * 256 + t, and stores them to a.src when that is given. Every phase issues
+// the LDS reads (or CASes) of a thread's four positions together before waiting on any.
+template <typename CodeT, typename Bar>
+__device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const ResolveArgs& a,
+                                              int64_t row, int chunk, int t, Bar bar,
+                                              int32_t (&src)[kPer]) {
+  const int lane = t & 63;
   const CodeT SENT = sentinel<CodeT>();
   const CodeT* qrow = static_cast<const CodeT*>(a.qc) + row * a.T;
   const CodeT* krow = static_cast<const CodeT*>(a.kc) + row * a.T;
@@ -297,14 +345,16 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
   const int n_here = static_cast<int>(a.T - c0 < kChunk ? a.T - c0 : kChunk);
 
   CodeT q[kPer], kk[kPer];
+  bool act[kPer];
 #pragma unroll
   for (int p = 0; p < kPer; ++p) {
     const int o = p * kThreads + t;
-    q[p] = o < n_here ? qrow[c0 + o] : CodeT(0);
-    kk[p] = o < n_here ? krow[c0 + o] : CodeT(0);
+    act[p] = o < n_here;
+    q[p] = act[p] ? qrow[c0 + o] : CodeT(0);
+    kk[p] = act[p] ? krow[c0 + o] : CodeT(0);
   }
-  // Keys before the chunk stream in batches of 1024 (4 per thread), the next batch loaded
-  // while the current one is looked up; c0 is a multiple of the batch.
+  // Keys before the chunk stream in batches of 1024 (4 per thread), latest batch first, the
+  // next batch loaded while the current one is looked up; c0 is a multiple of the batch.
   constexpr int kBatch = 4 * kThreads;
   CodeT nxt[4];
   auto load_batch = [&](int32_t j0) {
@@ -324,7 +374,7 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
       for (int e = 0; e < 4; ++e) nxt[e] = krow[j0 + e * kThreads + t];
     }
   };
-  if (c0 > 0) load_batch(0);
+  if (c0 > 0) load_batch(c0 - kBatch);
 
   for (int x = t; x < kSlots; x += kThreads) s.code[x] = SENT;
   for (int x = t; x <= kSlots; x += kThreads) {
@@ -336,111 +386,118 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
     s.mbits[x] = 0;
   }
   if (t == 0) s.sent_used = 0;
-  __syncthreads();
+  bar();
 
   // 1. the chunk's query codes -> table slots; the sentinel code has its own slot kSlots
+  // One position after another: a code inserted for an earlier position is usually found
+  // by a plain read, which keeps CAS traffic on popular codes low.
   int qs[kPer];
 #pragma unroll
   for (int p = 0; p < kPer; ++p) {
     qs[p] = kSlots;
-    if (p * kThreads + t >= n_here) continue;
+    if (!act[p]) continue;
     if (q[p] == SENT) {
       s.sent_used = 1;
       continue;
     }
-    qs[p] = table_claim<CodeT, kBucketLog>(s.code, q[p], SENT, hash32<kBucketLog>(fold(q[p])));
+    bool ins;
+    qs[p] = table_claim<CodeT, kBuckets>(s.code, q[p], SENT, bucket_of<kBuckets>(fold(q[p])), ins);
   }
-  __syncthreads();
+  bar();
 
   const bool sent_used = s.sent_used != 0;
-  // slot of key code c (first bucket b already read into x) among the query codes, or -1
-  auto find_code = [&](CodeT c, int b, CodeT (&x)[4]) -> int {
-    if (c == SENT) return sent_used ? kSlots : -1;
-    return table_find<CodeT, kBucketLog>(s.code, c, SENT, b, x);
+  // slots among the query codes of 4 key codes (-1 = no query of the chunk asks for it)
+  auto find_codes = [&](const CodeT (&c)[4], int (&sl)[4]) {
+    find4<CodeT, kBuckets>(s.code, c, SENT, sl);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (c[i] == SENT) sl[i] = sent_used ? kSlots : -1;
   };
 
-  // 2a. keys inside the chunk: each sets its lane in its (code, word) mask
+  // 2a. keys inside the chunk: each sets its lane in its (code, word) mask; the key that
+  // creates a (code, word) entry also sets the word's bit in the code's summary
   {
-    int b[kPer];
-    CodeT x[kPer][4];
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {  // first bucket reads of all 4 positions together
-      b[p] = hash32<kBucketLog>(fold(kk[p]));
-      read_bucket(s.code, b[p], x[p]);
-    }
+    int sl[kPer];
+    find_codes(kk, sl);
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
-      const int o = p * kThreads + t;
-      if (o >= n_here) continue;
-      const int sl = find_code(kk[p], b[p], x[p]);
-      if (sl < 0) continue;
-      const int wd = o >> 6;
-      const uint32_t key = (static_cast<uint32_t>(sl) << 5) | wd;
-      const int m = table_claim<uint32_t, kMapBucketLog>(s.mkey, key, kMapEmpty,
-                                                         hash32<kMapBucketLog>(key));
+      if (!act[p] || sl[p] < 0) continue;
+      const int wd = (p * kThreads + t) >> 6;
+      const uint32_t key = (static_cast<uint32_t>(sl[p]) << 4) | wd;
+      bool ins;
+      const int m = table_claim<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty,
+                                                       bucket_of<kMapBuckets>(key), ins);
       atomicOr(reinterpret_cast<unsigned long long*>(&s.mbits[m]), 1ull << lane);
-      atomicOr(&s.summ[sl], 1u << wd);
+      if (ins)
+        atomicOr(reinterpret_cast<uint32_t*>(&s.summ[sl[p] & ~1]), (1u << wd) << (16 * (sl[p] & 1)));
     }
   }
-  // 2b. keys before the chunk raise their code's latest position
-  for (int32_t j0 = 0; j0 < c0; j0 += kBatch) {
+  // 2b. keys before the chunk raise their code's latest position. Walking backwards, a code
+  // whose latest position is already known skips the atomic, so only the first batch that
+  // holds a popular code contends on its slot.
+  for (int32_t j0 = c0 - kBatch; j0 >= 0; j0 -= kBatch) {
     CodeT cur[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) cur[e] = nxt[e];
-    if (j0 + kBatch < c0) load_batch(j0 + kBatch);
-    int b[4];
-    CodeT x[4][4];
+    if (j0 > 0) load_batch(j0 - kBatch);
+    int sl[4];
+    find_codes(cur, sl);
+    int32_t known[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) known[e] = s.pos[sl[e] >= 0 ? sl[e] : kSlots];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      b[e] = hash32<kBucketLog>(fold(cur[e]));
-      read_bucket(s.code, b[e], x[e]);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int sl = find_code(cur[e], b[e], x[e]);
-      if (sl >= 0) atomicMax(&s.pos[sl], a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t);
+      const int32_t j = a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
+      if (sl[e] >= 0 && known[e] < j) atomicMax(&s.pos[sl[e]], j);
     }
   }
-  __syncthreads();
+  bar();
 
   // 3. resolve: the latest earlier lane of the own word, else the latest earlier word of the
   // chunk holding the code, else the latest position before the chunk
-  int32_t src[kPer];
   {
-    int mb[kPer];
-    uint32_t mx[kPer][4], key0[kPer];
+    int m[kPer];
+    uint32_t key[kPer];
 #pragma unroll
-    for (int p = 0; p < kPer; ++p) {  // first map reads of every position's own (code, word)
-      key0[p] = (static_cast<uint32_t>(qs[p]) << 5) | ((p * kThreads + t) >> 6);
-      mb[p] = hash32<kMapBucketLog>(key0[p]);
-      read_bucket(s.mkey, mb[p], mx[p]);
+    for (int p = 0; p < kPer; ++p)
+      key[p] = (static_cast<uint32_t>(qs[p]) << 4) | ((p * kThreads + t) >> 6);
+    find4<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty, m);
+    uint64_t bits[kPer];
+    uint32_t words[kPer];
+    int32_t before[kPer];
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {  // every read a position may need, issued together
+      bits[p] = s.mbits[m[p] >= 0 ? m[p] : 0];
+      words[p] = s.summ[qs[p]];
+      before[p] = s.pos[qs[p]];
     }
+    uint32_t key2[kPer];
+    bool second[kPer];
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
-      const int o = p * kThreads + t;
-      src[p] = -1;
-      if (o >= n_here) continue;
-      const uint32_t sl = static_cast<uint32_t>(qs[p]);
-      const int wd = o >> 6;
-      const int m = table_find<uint32_t, kMapBucketLog>(s.mkey, key0[p], kMapEmpty, mb[p], mx[p]);
-      const uint64_t below = m >= 0 ? (s.mbits[m] & ((1ull << lane) - 1)) : 0;
-      if (below) {
+      const int wd = (p * kThreads + t) >> 6;
+      const uint64_t below = m[p] >= 0 ? (bits[p] & ((1ull << lane) - 1)) : 0;
+      const uint32_t w_below = words[p] & ((1u << wd) - 1);
+      second[p] = false;
+      key2[p] = kMapEmpty;
+      if (!act[p]) {
+        src[p] = -1;
+      } else if (below) {
         src[p] = c0 + (wd << 6) + 63 - __clzll(below);
-        continue;
-      }
-      const uint32_t words = s.summ[sl] & ((1u << wd) - 1);
-      if (words) {
-        const int w2 = 31 - __clz(words);
-        const uint32_t key2 = (sl << 5) | w2;
-        uint32_t y2[4];
-        const int b2 = hash32<kMapBucketLog>(key2);
-        read_bucket(s.mkey, b2, y2);
-        const int m2 = table_find<uint32_t, kMapBucketLog>(s.mkey, key2, kMapEmpty, b2, y2);
-        src[p] = c0 + (w2 << 6) + 63 - __clzll(s.mbits[m2]);
+      } else if (w_below) {
+        const int w2 = 31 - __clz(w_below);
+        second[p] = true;
+        key2[p] = (static_cast<uint32_t>(qs[p]) << 4) | w2;
+        src[p] = c0 + (w2 << 6);
       } else {
-        src[p] = s.pos[sl];
+        src[p] = before[p];
       }
     }
+    int m2[kPer];
+    find4<uint32_t, kMapBuckets>(s.mkey, key2, kMapEmpty, m2);
+#pragma unroll
+    for (int p = 0; p < kPer; ++p)
+      if (second[p]) src[p] += 63 - __clzll(s.mbits[m2[p]]);
   }
   if (a.src != nullptr) {
 #pragma unroll
@@ -453,15 +510,33 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
         static_cast<int32_t*>(a.src)[row * a.T + c0 + o] = src[p];
     }
   }
+}
 
+// One workgroup (256 threads) per (row, chunk): resolve, then (VEC > 0) gather the chunk's
+// value rows. XCD-aware work mapping: every chunk of row r runs on XCD r % 8, which then keeps
+// that row's key codes and value rows in its own L2; the heaviest chunks (latest) go first.
+template <typename CodeT, int VEC>
+__global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
+  __shared__ ResolveLds<CodeT> s;
+  const int bid = blockIdx.x;
+  const int xcd = bid % kNumXcd;
+  const int k = bid / kNumXcd;
+  const int chunk = a.nchunks - 1 - (k % a.nchunks);
+  const int64_t row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
+  if (row >= a.N) return;
+  const int t = threadIdx.x;
+  int32_t src[kPer];
+  resolve_chunk(s, a, row, chunk, t, [] { __syncthreads(); }, src);
   if constexpr (VEC > 0) {
     int32_t* srcs = reinterpret_cast<int32_t*>(s.mbits);  // the masks are dead now
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < kPer; ++p) srcs[p * kThreads + t] = src[p];
     __syncthreads();
-    gather_rows<VEC, 8>(a.g, row, c0, n_here, t, kThreads,
-                        [&](uint32_t r) -> int64_t { return srcs[r]; });
+    const int32_t c0 = chunk * kChunk;
+    const int n_here = static_cast<int>(a.T - c0 < kChunk ? a.T - c0 : kChunk);
+    gather_rows<VEC, 8, 12>(a.g, row, c0, n_here, t, kThreads,
+                            [&](uint32_t r) -> int64_t { return srcs[r]; });
   }
 }
 
@@ -493,7 +568,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherOnlyArgs a) {
                                : static_cast<const int32_t*>(a.src)[at];
   }
   __syncthreads();
-  gather_rows<VEC, 8>(a.g, row, c0, nrows, threadIdx.x, blockDim.x,
+  gather_rows<VEC, 8, 12>(a.g, row, c0, nrows, threadIdx.x, blockDim.x,
                       [&](uint32_t r) -> int64_t { return ssrc[r]; });
 }
 
@@ -532,6 +607,9 @@ int fill_gather(GatherArgs& g, const void* v, int32_t dtype, int64_t H, int64_t 
   g.y_st = y_st * es;
   g.pieces = static_cast<uint32_t>(rb / vec);
   g.pdiv = FastDiv(g.pieces);
+  g.plog = -1;
+  for (int l = 0; l <= 6; ++l)
+    if (g.pieces == (1u << l)) g.plog = l;
   g.miss = miss;
   g.dtype = dtype;
   *vec_out = vec;
@@ -540,10 +618,9 @@ int fill_gather(GatherArgs& g, const void* v, int32_t dtype, int64_t H, int64_t 
 
 template <typename CodeT>
 int launch_resolve(ResolveArgs& a, int vec, hipStream_t st) {
-  const int64_t groups = (a.N + kNumXcd - 1) / kNumXcd;
-  const int64_t grid = groups * kNumXcd * a.nchunks;
-  LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows x chunks (%lld)", (long long)grid);
   a.kvec = (aligned(a.kc, 16) && (a.T * static_cast<int64_t>(sizeof(CodeT))) % 16 == 0) ? 1 : 0;
+  const int64_t grid = (a.N + kNumXcd - 1) / kNumXcd * kNumXcd * a.nchunks;
+  LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows x chunks (%lld)", (long long)grid);
   switch (vec) {
     case 0: resolve_kernel<CodeT, 0><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
     case 16: resolve_kernel<CodeT, 16><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
