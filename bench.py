@@ -42,6 +42,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16,
                     help="(b, h) rows of the workload timed for the CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one plain device copy of the value tensor (known bytes), "
+                         "to calibrate profiler memory counters")
     return ap.parse_args()
 
 
@@ -102,6 +105,9 @@ def bench_prefill(a):
     y = torch.empty_like(vd)
     src = torch.empty((B, H, T), dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
+    if a.copy_probe:
+        y.copy_(vd)                      # reads and writes exactly vd.numel() * 2 bytes
+        torch.cuda.synchronize()
     for _ in range(a.warmup):
         launch_hard(qd, kd, vd, y, src)
     torch.cuda.synchronize()
