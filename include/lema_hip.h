@@ -76,6 +76,23 @@ int lema_gather(const void* v, int32_t dtype, int64_t B, int64_t H, int64_t T, i
                 void* y, int64_t y_sb, int64_t y_sh, int64_t y_st, int32_t miss,
                 void* stream);
 
+/* One exchange against the shared open-addressing store in device memory.
+ * Replaces store_exchange, code/lema/csrc/store.cpp:122-162 (bound as lema_store.exchange,
+ * store.cpp:164-167, called from HashStore.exchange, code/lema/cache.py:184-201).
+ *   table   [cap, 16 + vbytes] bytes, the reference's slot format ([code u64 | state u64 |
+ *           value]); all zeros = empty
+ *   items   i in [0, n): position i % T of partition i / T, group g0 + i / T; in position
+ *           order per partition: out[i] = value of (group, qc[i]) or zeros, then
+ *           (group, kc[i]) -> values[i], latest write wins
+ *   qc      n codes of code_bytes, or NULL to only insert (then out may be NULL)
+ *   values, out  [n, vbytes] bytes; vbytes % 8 == 0
+ *   counts  int64 per group: += newly claimed slots
+ *   full    int32 flag set to 1 when some key found no free slot (the reference raises
+ *           "hash table full" after such a pass; the caller checks the flag)             */
+int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, const void* kc,
+                        int32_t code_bytes, const void* values, void* out, int64_t n, int64_t T,
+                        int64_t g0, int64_t* counts, int32_t* full, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

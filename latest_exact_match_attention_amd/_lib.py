@@ -35,6 +35,8 @@ PROTOTYPES = {
                    _i64, _i64, _i32, _p, _i32, _p], ctypes.c_int),
     "lema_gather": ([_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i32, _p, _i64,
                      _i64, _i64, _i32, _p], ctypes.c_int),
+    "lema_store_exchange": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p, _p, _p],
+                            ctypes.c_int),
 }
 
 _LIB = None

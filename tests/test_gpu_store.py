@@ -1,0 +1,164 @@
+"""The HBM store against the reference's store semantics (code/tests/test_store.py pattern):
+every exchange output and every per-partition count must equal a per-partition dict with
+latest-write-wins, across chunked, decode-sized and one-shot calls; an overfull table raises
+"full"; the golden replay was produced by the reference's own store.cpp.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from latest_exact_match_attention_amd import lema_from_codes
+from latest_exact_match_attention_amd.cache import HashStore, LemaCache
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+D_V = 8                                   # uint16 rows: 16 bytes, as the reference test
+
+
+def run_dict_case(dev, seed, P, T, chunk, n_codes, capacity, code_dtype=torch.int64):
+    """code/tests/test_store.py:17-41 against the HBM store."""
+    rng = np.random.default_rng(seed)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=capacity, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    codes = rng.integers(0, n_codes, size=(2, P, T), dtype=np.int64) * 7919 % (n_codes + 2)
+    vals = rng.integers(0, 1 << 16, size=(P, T, D_V), dtype=np.uint16)
+    for lo in range(0, T, chunk):
+        hi = min(T, lo + chunk)
+        qc = np.ascontiguousarray(codes[0, :, lo:hi]).reshape(-1)
+        kc = np.ascontiguousarray(codes[1, :, lo:hi]).reshape(-1)
+        v = np.ascontiguousarray(vals[:, lo:hi]).reshape(-1, D_V)
+        out = torch.empty((qc.size, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev).to(code_dtype),
+                       torch.from_numpy(kc).to(dev).to(code_dtype),
+                       torch.from_numpy(v.view(np.int16)).to(dev), out, hi - lo, 0)
+        want = ref.exchange(qc, kc, v.view(np.uint8).reshape(-1, 2 * D_V), hi - lo, 0)
+        got = out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V)
+        assert np.array_equal(got, want), (seed, lo)
+    assert np.array_equal(store.counts.numpy(), ref.counts()), "entries per partition"
+    return store, ref
+
+
+def test_store_golden_replay(dev):
+    """Outputs and counts the reference's store.cpp produced for the same exchanges."""
+    g = np.load(GOLDEN / "store.npz")
+    codes, vals, chunks, cap = g["codes"], g["vals"], g["chunks"], int(g["cap"])
+    P, T, vb = vals.shape
+    store = HashStore(vb // 2, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    lo = 0
+    for c in chunks:
+        hi = lo + int(c)
+        qc = torch.from_numpy(np.ascontiguousarray(codes[0, :, lo:hi]).reshape(-1)).to(dev)
+        kc = torch.from_numpy(np.ascontiguousarray(codes[1, :, lo:hi]).reshape(-1)).to(dev)
+        v = torch.from_numpy(np.ascontiguousarray(vals[:, lo:hi]).reshape(-1, vb)).to(dev)
+        out = torch.empty_like(v)
+        store.exchange(qc, kc, v, out, hi - lo, 0)
+        assert np.array_equal(out.cpu().numpy().reshape(P, hi - lo, vb), g["out"][:, lo:hi])
+        lo = hi
+    assert np.array_equal(store.counts.numpy(), g["counts"])
+
+
+def test_store_chunks_of_500(dev):
+    store, ref = run_dict_case(dev, seed=0, P=200, T=2000, chunk=500, n_codes=400,
+                               capacity=90_000)
+    assert store.load() > 0.5
+    # the table itself: its published entries are exactly the dict's final content
+    grp, code, val = store.dump()
+    got = {(int(a), int(b)): bytes(c) for a, b, c in
+           zip(grp.cpu().numpy(), code.cpu().numpy(), val.cpu().numpy())}
+    want = {(p, k): bytes(v) for p, d in enumerate(ref.ref) for k, v in d.items()}
+    assert got == want
+
+
+def test_store_decode_sized(dev):
+    run_dict_case(dev, seed=1, P=64, T=300, chunk=1, n_codes=150, capacity=11_000)
+
+
+def test_store_one_shot(dev):
+    run_dict_case(dev, seed=2, P=400, T=1000, chunk=1000, n_codes=300, capacity=130_000)
+
+
+def test_store_long_call_spans_subchunks(dev):
+    """T = 2500 per call: three 1024-position sub-chunks in order within one exchange."""
+    run_dict_case(dev, seed=5, P=30, T=2500, chunk=2500, n_codes=60, capacity=6000,
+                  code_dtype=torch.int32)
+
+
+def test_store_overfull_raises(dev):
+    with pytest.raises(RuntimeError, match="full"):
+        run_dict_case(dev, seed=3, P=50, T=100, chunk=100, n_codes=100, capacity=1000)
+
+
+def test_store_contended_decode(dev):
+    """1024 partitions claiming slots of a small shared table every step (load ~0.9 at the
+    end): concurrent claims from every XCD must never hand one slot to two keys."""
+    P, steps, cap = 1024, 60, 70_000
+    rng = np.random.default_rng(9)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    for s in range(steps):
+        qc = rng.integers(0, 2**63, P, dtype=np.int64)
+        qc[::3] = rng.integers(0, 50, P)[::3]           # some queries hit earlier keys
+        kc = rng.integers(0, 50, P, dtype=np.int64) if s % 2 else rng.integers(0, 2**63, P)
+        v = rng.integers(0, 1 << 16, size=(P, D_V), dtype=np.uint16)
+        out = torch.empty((P, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev),
+                       torch.from_numpy(v.view(np.int16)).to(dev), out, 1, 0)
+        want = ref.exchange(qc, kc, v.view(np.uint8).reshape(-1, 2 * D_V), 1, 0)
+        assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want), s
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    grp, _, _ = store.dump()
+    assert grp.numel() == len(store)                   # every claimed slot published once
+
+
+def test_store_table_is_reference_format(dev):
+    """A table filled on the GPU is continued by the C restatement of store.cpp on the host
+    (same slot format and home-slot hash): the results stay those of the dict."""
+    rng = np.random.default_rng(4)
+    P, T, vb, cap = 16, 64, 16, 2048
+    store = HashStore(vb // 2, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    ref = oracle.DictStore(P, vb)
+    codes = rng.integers(0, 40, size=(4, P, T), dtype=np.int64)
+    vals = rng.integers(0, 256, size=(2, P, T, vb), dtype=np.uint8)
+    qc, kc = codes[0].reshape(-1), codes[1].reshape(-1)
+    v = vals[0].reshape(-1, vb)
+    out = torch.empty((P * T, vb), dtype=torch.uint8, device=dev)
+    store.exchange(torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev),
+                   torch.from_numpy(v).to(dev), out, T, 0)
+    assert np.array_equal(out.cpu().numpy(), ref.exchange(qc, kc, v, T, 0))
+    host = oracle.HostStore(vb, P, cap)
+    host.table[:] = store.table.cpu().numpy()
+    host.counts[:] = store.counts.numpy()
+    qc2, kc2 = codes[2].reshape(-1), codes[3].reshape(-1)
+    v2 = vals[1].reshape(-1, vb)
+    out2 = np.empty_like(v2)
+    host.exchange(qc2, kc2, v2, out2, T, 0)
+    assert np.array_equal(out2, ref.exchange(qc2, kc2, v2, T, 0))
+    assert np.array_equal(host.counts, ref.counts())
+
+
+class _Cfg:
+    depth, num_heads, d_v = 2, 4, 16
+
+
+@pytest.mark.parametrize("step", [1, 7, 64, 300])
+def test_cache_chunked_equals_dense(dev, step):
+    """Fed through the store in any chunking, a layer retrieves what the dense op gathers
+    (values of matched keys; the store's miss is +0) -- code/tests/test_gpu.py:68-90 at the
+    op level."""
+    B, H, T, dv = 2, _Cfg.num_heads, 300, _Cfg.d_v
+    rng = np.random.default_rng(step)
+    qc = torch.from_numpy(rng.integers(0, 30, (B, H, T))).to(dev)
+    kc = torch.from_numpy(rng.integers(0, 30, (B, H, T))).to(dev)
+    v = torch.randn(B, H, T, dv, device=dev, dtype=torch.bfloat16)
+    dense, src = lema_from_codes(qc, kc, v, return_src=True)
+    dense = torch.where((src >= 0).unsqueeze(-1), dense, torch.zeros_like(dense))
+    cache = LemaCache(_Cfg, dtype=torch.bfloat16, max_cache_len=T, batch=B, device=dev)
+    parts = [cache.layer(1).exchange(qc[:, :, s:s + step], kc[:, :, s:s + step],
+                                     v[:, :, s:s + step]) for s in range(0, T, step)]
+    got = torch.cat(parts, dim=2)
+    assert torch.equal(got.view(torch.int16), dense.view(torch.int16))
+    assert cache.entries() == int(cache.counts().sum()) > 0
+    assert cache.counts()[0].sum() == 0                 # layer 0's partitions untouched
