@@ -3,8 +3,9 @@
 // driven by code/lema/cache.py:129-302).
 //
 // Table format -- identical to the reference's, so a table is interchangeable byte for byte:
-// slot s is [code u64 | state u64 | value bytes] at s * (16 + vbytes); state 0 = free, 1 =
-// being filled, group + 2 = published. The home slot of (group, code) is Lemire's fastrange of
+// slot s is [code u64 | state u64 | value bytes] at s * (16 + vbytes); state 0 = free,
+// group + 2 = taken (the reference also passes through 1 while a slot is filled; no completed
+// exchange leaves it, and this store never writes it). The home slot of (group, code) is Lemire's fastrange of
 // the splitmix64 finaliser of code ^ (group * 2^64/phi) (store.cpp:58-71); probing is linear with
 // wrap-around. A zeroed allocation is an empty table.
 //
@@ -14,26 +15,34 @@
 // grows by the newly claimed slots; a key that finds no free slot sets *full.
 //
 // GPU execution. Partitions run concurrently; the only cross-partition interaction is slot
-// claiming, done with a device-scope CAS on the state word (free -> being filled), after which
-// the claimer writes code and value and publishes group + 2. A reader never needs another
-// partition's code or value: it skips slots whose state is not its own tag and stops at a
-// free slot. Its own entries come from earlier kernels (coherent at the kernel boundary) or
-// from its own workgroup, and every slot in front of an entry on its probe path was occupied
-// before the entry was made, so a stale read can only show a free slot where another
-// partition is claiming -- plain header reads are hints, the CAS decides.
-//   * T == 1 (a decode step): one kernel; 8 lanes per item probe an 8-slot window per round
-//     trip (one ballot), look the query up, then insert the key.
+// claiming: a device-scope CAS of the state word from free straight to the claimer's tag, then
+// plain stores of code and value. No reader in the same kernel ever reads a slot it did not
+// find before the kernel started -- another partition's slot is skipped on its tag, and a
+// partition's own new slots are only probed for "free" -- so the claim needs no intermediate
+// state and no fence; the kernel boundary publishes code and value to later exchanges. Every
+// slot in front of an entry on its probe path was occupied before the entry was made, so a
+// stale read can only show a free slot where someone is claiming: header reads are hints, the
+// CAS decides.
+//   * T == 1 (a decode step): one kernel; 8 lanes per item read the query's and the key's
+//     first 8-slot windows together (one ballot each), look the query up, then update the
+//     key's entry or claim a slot for it.
 //   * T >= 2: sub-chunks of up to 1024 positions, one launch per sub-chunk (in order), one
 //     workgroup per partition: in-chunk matches come from the LDS resolver, other queries from
-//     the table, then -- after a workgroup barrier, so no query sees a later key -- each key
-//     code's last occurrence in the sub-chunk is inserted.
+//     the table; after a workgroup barrier (no query may see a later key) each key code's
+//     last occurrence overwrites its existing entry, and after another barrier the codes that
+//     had none claim new slots.
 #include "resolve_core.h"
 
 namespace lema {
 namespace {
 
-constexpr uint64_t kStateEmpty = 0, kStateLocked = 1;
-constexpr int kGroup = 8;  // lanes probing one item together
+constexpr uint64_t kStateEmpty = 0;
+// Lanes probing one item together: one window of kGroup slots per round trip.
+#ifndef LEMA_STORE_GROUP
+#define LEMA_STORE_GROUP 8
+#endif
+constexpr int kGroup = LEMA_STORE_GROUP;
+static_assert(kGroup == 4 || kGroup == 8 || kGroup == 16 || kGroup == 32, "probe group width");
 
 __device__ __forceinline__ uint64_t splitmix_fin(uint64_t x) {
   x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -102,17 +111,17 @@ __device__ __forceinline__ Window read_window(const StoreArgs& a, int64_t base, 
     m = st == tag && hdr[0] == code;
     e = st == kStateEmpty;
   }
-  const uint32_t mask = (1u << kGroup) - 1;
-  return Window{static_cast<uint32_t>(__ballot(m) >> gbase) & mask,
-                static_cast<uint32_t>(__ballot(e) >> gbase) & mask};
+  const uint64_t mask = kGroup == 64 ? ~0ull : ((1ull << kGroup) - 1);
+  return Window{static_cast<uint32_t>((__ballot(m) >> gbase) & mask),
+                static_cast<uint32_t>((__ballot(e) >> gbase) & mask)};
 }
 
-// Slot of (tag, code) or -1 (code/lema/csrc/store.cpp:84-93). Group-uniform.
-__device__ int64_t group_lookup(const StoreArgs& a, uint64_t code, uint64_t tag, int gl,
-                                int gbase) {
-  int64_t base = home_slot(code, tag - 2, a.cap);
+// Slot of (tag, code) or -1 (code/lema/csrc/store.cpp:84-93), starting from the first window
+// w0 read at `base` = home. Group-uniform.
+__device__ int64_t group_lookup(const StoreArgs& a, uint64_t code, uint64_t tag, int64_t base,
+                                Window w0, int gl, int gbase) {
   for (int64_t left = a.cap; left > 0; left -= kGroup) {
-    const Window w = read_window(a, base, left, code, tag, gl, gbase);
+    const Window w = left == a.cap ? w0 : read_window(a, base, left, code, tag, gl, gbase);
     const int fm = w.match ? __ffs(w.match) - 1 : kGroup;
     const int fe = w.empty ? __ffs(w.empty) - 1 : kGroup;
     if (fm < fe) {
@@ -126,14 +135,15 @@ __device__ int64_t group_lookup(const StoreArgs& a, uint64_t code, uint64_t tag,
   return -1;
 }
 
-// Insert (tag, code) -> value (code/lema/csrc/store.cpp:97-117): 1 = claimed a new slot, 0 =
-// overwrote the partition's own entry, -1 = probed every slot without room. Group-uniform.
+// Insert (tag, code) -> value (code/lema/csrc/store.cpp:97-117), starting from the first
+// window w0 read at `base` = home: 1 = claimed a new slot, 0 = overwrote the partition's own
+// entry, -1 = probed every slot without room. With `claim_only` the key is known to be absent
+// and only free slots are looked for. Group-uniform.
 __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, const uint8_t* value,
-                            int gl, int gbase) {
-  int64_t base = home_slot(code, tag - 2, a.cap);
+                            int64_t base, Window w0, bool claim_only, int gl, int gbase) {
   for (int64_t left = a.cap; left > 0; left -= kGroup) {
-    const Window w = read_window(a, base, left, code, tag, gl, gbase);
-    const int fm = w.match ? __ffs(w.match) - 1 : kGroup;
+    const Window w = left == a.cap ? w0 : read_window(a, base, left, code, tag, gl, gbase);
+    const int fm = (!claim_only && w.match) ? __ffs(w.match) - 1 : kGroup;
     uint32_t empty = w.empty;
     if (fm < kGroup && (!empty || fm < __ffs(empty) - 1)) {
       int64_t s = base + fm;
@@ -147,15 +157,11 @@ __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, con
       if (s >= a.cap) s -= a.cap;
       unsigned long long old = 0;
       if (gl == e)
-        old = atomicCAS(reinterpret_cast<unsigned long long*>(state_ptr(a, s)), kStateEmpty,
-                        kStateLocked);
+        old = atomicCAS(reinterpret_cast<unsigned long long*>(state_ptr(a, s)), kStateEmpty, tag);
       const bool won = __shfl(old == kStateEmpty ? 1 : 0, gbase + e) != 0;
       if (won) {
         if (gl == e) *reinterpret_cast<uint64_t*>(a.table + s * a.stride) = code;
         group_copy(a, a.table + s * a.stride + 16, value, gl);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        if (gl == e)
-          __hip_atomic_store(state_ptr(a, s), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return 1;
       }
       empty &= ~(1u << e);
@@ -173,12 +179,19 @@ __global__ __launch_bounds__(256) void store_step_kernel(StoreArgs a) {
   const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
   if (i >= a.n) return;  // whole groups only: n is a count of items, groups are aligned
   const uint64_t tag = static_cast<uint64_t>(a.g0 + i) + 2;
+  const uint64_t kcode = code_at(a.kc, a.code_bytes, i);
+  const int64_t khome = home_slot(kcode, tag - 2, a.cap);
+  const uint64_t qcode = a.qc != nullptr ? code_at(a.qc, a.code_bytes, i) : 0;
+  const int64_t qhome = a.qc != nullptr ? home_slot(qcode, tag - 2, a.cap) : 0;
+  // the two first windows are independent: both reads are in flight together
+  const Window wk = read_window(a, khome, a.cap, kcode, tag, gl, gbase);
+  const Window wq = a.qc != nullptr ? read_window(a, qhome, a.cap, qcode, tag, gl, gbase)
+                                    : Window{0u, 0u};
   if (a.qc != nullptr) {
-    const int64_t s = group_lookup(a, code_at(a.qc, a.code_bytes, i), tag, gl, gbase);
+    const int64_t s = group_lookup(a, qcode, tag, qhome, wq, gl, gbase);
     group_copy(a, a.out + i * a.vbytes, s >= 0 ? a.table + s * a.stride + 16 : nullptr, gl);
   }
-  const int r = group_insert(a, code_at(a.kc, a.code_bytes, i), tag, a.values + i * a.vbytes,
-                             gl, gbase);
+  const int r = group_insert(a, kcode, tag, a.values + i * a.vbytes, khome, wk, false, gl, gbase);
   if (gl == 0) {
     if (r > 0) atomicAdd(&a.counts[a.g0 + i], 1ull);
     if (r < 0) atomicOr(a.full, 1);
@@ -251,19 +264,37 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
       if (j >= 0) {
         group_copy(a, dst, a.values + (first + j) * a.vbytes, gl);
       } else {
-        const int64_t sl = group_lookup(a, code_at(a.qc, a.code_bytes, first + o), tag, gl, gbase);
+        const uint64_t c = code_at(a.qc, a.code_bytes, first + o);
+        const int64_t h = home_slot(c, tag - 2, a.cap);
+        const int64_t sl = group_lookup(a, c, tag, h, read_window(a, h, a.cap, c, tag, gl, gbase),
+                                        gl, gbase);
         group_copy(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, gl);
       }
     }
   }
   __syncthreads();  // every query of this partition has read the table before any insert
 
-  // 4. insert each key code's last occurrence
-  int added = 0;
+  // 4. each key code's last occurrence overwrites its existing entry; codes without one are
+  // marked (klast = 2) and, once no sibling can still be looking entries up, claim a slot
   for (int o = grp; o < n; o += kGroups) {
     if (!klast[o]) continue;
-    const int r = group_insert(a, code_at(a.kc, a.code_bytes, first + o), tag,
-                               a.values + (first + o) * a.vbytes, gl, gbase);
+    const uint64_t c = code_at(a.kc, a.code_bytes, first + o);
+    const int64_t h = home_slot(c, tag - 2, a.cap);
+    const int64_t sl = group_lookup(a, c, tag, h, read_window(a, h, a.cap, c, tag, gl, gbase),
+                                    gl, gbase);
+    if (sl >= 0)
+      group_copy(a, a.table + sl * a.stride + 16, a.values + (first + o) * a.vbytes, gl);
+    else if (gl == 0)
+      klast[o] = 2;
+  }
+  __syncthreads();
+  int added = 0;
+  for (int o = grp; o < n; o += kGroups) {
+    if (klast[o] != 2) continue;
+    const uint64_t c = code_at(a.kc, a.code_bytes, first + o);
+    const int64_t h = home_slot(c, tag - 2, a.cap);
+    const int r = group_insert(a, c, tag, a.values + (first + o) * a.vbytes, h,
+                               read_window(a, h, a.cap, c, tag, gl, gbase), true, gl, gbase);
     if (r > 0) ++added;
     if (r < 0 && gl == 0) atomicOr(a.full, 1);
   }

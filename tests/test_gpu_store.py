@@ -162,3 +162,38 @@ def test_cache_chunked_equals_dense(dev, step):
     assert torch.equal(got.view(torch.int16), dense.view(torch.int16))
     assert cache.entries() == int(cache.counts().sum()) > 0
     assert cache.counts()[0].sum() == 0                 # layer 0's partitions untouched
+
+
+def test_decode_steps_in_a_graph_equal_eager(dev):
+    """Decode steps captured into one HIP graph and replayed produce exactly what the eager
+    steps produce (code/tests/test_gpu.py:117-141 at the store level); the graph is replayed
+    once, between eager host work and a synchronisation."""
+    P, steps, cap, dv = 256, 24, 40_000, 24
+    gen = torch.Generator(device=dev).manual_seed(3)
+    pre_k = torch.randint(0, 2**32, (P * 64,), dtype=torch.int64, device=dev, generator=gen)
+    pre_v = torch.randn((P * 64, dv), device=dev, generator=gen).to(torch.bfloat16)
+    qc = torch.randint(0, 2**32, (steps, P), dtype=torch.int64, device=dev, generator=gen)
+    qc[:, ::4] = pre_k.view(P, 64)[::4, :steps].t()      # every 4th partition hits a prefill key
+    kc = torch.randint(0, 2**32, (steps, P), dtype=torch.int64, device=dev, generator=gen)
+    vv = torch.randn((steps, P, dv), device=dev, generator=gen).to(torch.bfloat16)
+    stores = [HashStore(dv, groups=P, dtype=torch.bfloat16, capacity=cap, device=dev)
+              for _ in range(2)]
+    for st in stores:
+        st.exchange(None, pre_k, pre_v, None, 64, 0)
+    eager = torch.empty_like(vv)
+    for s in range(steps):
+        stores[0].exchange(qc[s], kc[s], vv[s], eager[s], 1, 0)
+    graphed = torch.empty_like(vv)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for s in range(steps):
+            stores[1].exchange(qc[s], kc[s], vv[s], graphed[s], 1, 0, check=False)
+    assert int(stores[1].counts_device.sum()) == P * 64      # capture ran nothing
+    torch.randn(1000, device=dev).sum().item()               # eager work in between
+    g.replay()
+    torch.cuda.synchronize()
+    stores[1].check_full()
+    assert torch.equal(graphed.view(torch.int16), eager.view(torch.int16))
+    assert torch.equal(stores[1].counts, stores[0].counts)
+    assert (eager[:, ::4] != 0).any(-1).float().mean() > 0.9
