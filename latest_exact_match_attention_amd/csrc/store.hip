@@ -37,12 +37,26 @@ namespace lema {
 namespace {
 
 constexpr uint64_t kStateEmpty = 0;
-// Lanes probing one item together: one window of kGroup slots per round trip.
+// Lanes probing one item together, one window of that many slots per round trip: a decode
+// step gives each item kStepGroup lanes (wide windows: few items ever need a second one), a
+// chunk workgroup kGroup lanes per item (many items in flight).
 #ifndef LEMA_STORE_GROUP
 #define LEMA_STORE_GROUP 8
 #endif
+#ifndef LEMA_STEP_GROUP
+#define LEMA_STEP_GROUP 32
+#endif
+#ifndef LEMA_STEP_BLOCK
+#define LEMA_STEP_BLOCK 128
+#endif
 constexpr int kGroup = LEMA_STORE_GROUP;
-static_assert(kGroup == 4 || kGroup == 8 || kGroup == 16 || kGroup == 32, "probe group width");
+constexpr int kStepGroup = LEMA_STEP_GROUP;
+constexpr int kStepBlock = LEMA_STEP_BLOCK;  // threads per decode-step workgroup
+static_assert(kGroup == 4 || kGroup == 8 || kGroup == 16 || kGroup == 32 || kGroup == 64,
+              "probe group width");
+static_assert(kStepGroup == 8 || kStepGroup == 16 || kStepGroup == 32 || kStepGroup == 64,
+              "probe group width");
+static_assert(kStepBlock % 64 == 0 && kStepBlock >= kStepGroup, "whole wavefronts of groups");
 
 __device__ __forceinline__ uint64_t splitmix_fin(uint64_t x) {
   x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -66,7 +80,10 @@ struct StoreArgs {
   int64_t n, T, g0;
   int64_t s0;   // first position of the sub-chunk (T >= 2)
   int32_t len;  // positions in the sub-chunk
-  int32_t piece;  // 16 or 8: value bytes copied per lane
+  int32_t piece;   // 16 or 8: value bytes copied per lane
+  int32_t pieces;  // vbytes / piece
+  bool pre;        // piece 16 and pieces <= kStepGroup: a decode step preloads the value row
+  bool spec;       // piece 16 and pieces <= kSpecPieces: its query window reads whole slots
   unsigned long long* counts;
   int32_t* full;
 };
@@ -81,10 +98,11 @@ __device__ __forceinline__ uint64_t* state_ptr(const StoreArgs& a, int64_t s) {
 }
 
 // Copy one value row with the group's lanes (src null: write zeros).
+template <int G>
 __device__ __forceinline__ void group_copy(const StoreArgs& a, uint8_t* dst, const uint8_t* src,
                                            int gl) {
   const int pieces = static_cast<int>(a.vbytes / a.piece);
-  for (int k = gl; k < pieces; k += kGroup) {
+  for (int k = gl; k < pieces; k += G) {
     if (a.piece == 16) {
       const u32x4 v = src ? *reinterpret_cast<const u32x4*>(src + 16 * k) : u32x4{0u, 0u, 0u, 0u};
       *reinterpret_cast<u32x4*>(dst + 16 * k) = v;
@@ -95,11 +113,18 @@ __device__ __forceinline__ void group_copy(const StoreArgs& a, uint8_t* dst, con
   }
 }
 
-// The window of kGroup slots starting at `base` (wrapping); lane gl reads slot base + gl.
+// The window of G slots starting at `base` (wrapping); lane gl reads slot base + gl.
 // Lanes beyond the `left` slots still to probe report nothing. Returns this group's bits.
 struct Window {
-  uint32_t match, empty;
+  uint64_t match, empty;
 };
+__device__ __forceinline__ int first_bit(uint64_t x) { return __ffsll(static_cast<unsigned long long>(x)) - 1; }
+template <int G>
+__device__ __forceinline__ Window window_bits(bool m, bool e, int gbase) {
+  const uint64_t mask = G == 64 ? ~0ull : ((1ull << G) - 1);
+  return Window{(__ballot(m) >> gbase) & mask, (__ballot(e) >> gbase) & mask};
+}
+template <int G>
 __device__ __forceinline__ Window read_window(const StoreArgs& a, int64_t base, int64_t left,
                                               uint64_t code, uint64_t tag, int gl, int gbase) {
   bool m = false, e = false;
@@ -111,87 +136,174 @@ __device__ __forceinline__ Window read_window(const StoreArgs& a, int64_t base, 
     m = st == tag && hdr[0] == code;
     e = st == kStateEmpty;
   }
-  const uint64_t mask = kGroup == 64 ? ~0ull : ((1ull << kGroup) - 1);
-  return Window{static_cast<uint32_t>((__ballot(m) >> gbase) & mask),
-                static_cast<uint32_t>((__ballot(e) >> gbase) & mask)};
+  return window_bits<G>(m, e, gbase);
 }
 
-// Slot of (tag, code) or -1 (code/lema/csrc/store.cpp:84-93), starting from the first window
-// w0 read at `base` = home. Group-uniform.
+// The first window read as whole slots (header and value, 16-byte pieces): a hit's value is
+// then already in lane `match`'s registers. Needs 16-byte slots and at most kSpecPieces pieces.
+constexpr int kSpecPieces = 4;
+template <int G>
+__device__ __forceinline__ Window read_window_slots(const StoreArgs& a, int64_t base, uint64_t code,
+                                                    uint64_t tag, int gl, int gbase,
+                                                    u32x4 (&val)[kSpecPieces]) {
+  bool m = false, e = false;
+  if (gl < a.cap) {
+    int64_t s = base + gl;
+    if (s >= a.cap) s -= a.cap;
+    const uint8_t* slot = a.table + s * a.stride;
+    const u32x4 hdr = *reinterpret_cast<const u32x4*>(slot);
+#pragma unroll
+    for (int k = 0; k < kSpecPieces; ++k)
+      if (k < a.pieces) val[k] = *reinterpret_cast<const u32x4*>(slot + 16 + 16 * k);
+    const uint64_t c = (static_cast<uint64_t>(hdr[1]) << 32) | hdr[0];
+    const uint64_t st = (static_cast<uint64_t>(hdr[3]) << 32) | hdr[2];
+    m = st == tag && c == code;
+    e = st == kStateEmpty;
+  }
+  return window_bits<G>(m, e, gbase);
+}
+
+// Slot of (tag, code) or -1 (code/lema/csrc/store.cpp:84-93), starting from window w0 read at
+// `base` with `left` slots still unprobed. Group-uniform.
+template <int G>
 __device__ int64_t group_lookup(const StoreArgs& a, uint64_t code, uint64_t tag, int64_t base,
-                                Window w0, int gl, int gbase) {
-  for (int64_t left = a.cap; left > 0; left -= kGroup) {
-    const Window w = left == a.cap ? w0 : read_window(a, base, left, code, tag, gl, gbase);
-    const int fm = w.match ? __ffs(w.match) - 1 : kGroup;
-    const int fe = w.empty ? __ffs(w.empty) - 1 : kGroup;
+                                int64_t left, Window w0, int gl, int gbase) {
+  for (const int64_t left0 = left; left > 0; left -= G) {
+    const Window w = left == left0 ? w0 : read_window<G>(a, base, left, code, tag, gl, gbase);
+    const int fm = w.match ? first_bit(w.match) : G;
+    const int fe = w.empty ? first_bit(w.empty) : G;
     if (fm < fe) {
       const int64_t s = base + fm;
       return s >= a.cap ? s - a.cap : s;
     }
     if (w.empty) return -1;
-    base += kGroup;
+    base += G;
     if (base >= a.cap) base -= a.cap;
   }
   return -1;
 }
 
-// Insert (tag, code) -> value (code/lema/csrc/store.cpp:97-117), starting from the first
-// window w0 read at `base` = home: 1 = claimed a new slot, 0 = overwrote the partition's own
-// entry, -1 = probed every slot without room. With `claim_only` the key is known to be absent
-// and only free slots are looked for. Group-uniform.
+// Claim the first free slot of window `empty` (bits relative to `base`) for (tag, code):
+// the slot index, or -1 when every one of them was taken first by another claimer (a lost
+// race just marks that slot taken). The winner's lane writes the code; the caller the value.
+__device__ __forceinline__ int64_t claim_in_window(const StoreArgs& a, uint64_t code, uint64_t tag,
+                                                   int64_t base, uint64_t empty, int gl, int gbase) {
+  while (empty) {
+    const int e = first_bit(empty);
+    int64_t s = base + e;
+    if (s >= a.cap) s -= a.cap;
+    unsigned long long old = 0;
+    if (gl == e)
+      old = atomicCAS(reinterpret_cast<unsigned long long*>(state_ptr(a, s)), kStateEmpty, tag);
+    if (__shfl(old == kStateEmpty ? 1 : 0, gbase + e) != 0) {
+      if (gl == e) *reinterpret_cast<uint64_t*>(a.table + s * a.stride) = code;
+      return s;
+    }
+    empty &= ~(1ull << e);
+  }
+  return -1;
+}
+
+// Insert (tag, code) -> value (code/lema/csrc/store.cpp:97-117), starting from window w0 read
+// at `base` with `left` slots still unprobed: 1 = claimed a new slot, 0 = overwrote the
+// partition's own entry, -1 = probed every slot without room. With `claim_only` the key is
+// known to be absent and only free slots are looked for. Group-uniform.
+template <int G>
 __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, const uint8_t* value,
-                            int64_t base, Window w0, bool claim_only, int gl, int gbase) {
-  for (int64_t left = a.cap; left > 0; left -= kGroup) {
-    const Window w = left == a.cap ? w0 : read_window(a, base, left, code, tag, gl, gbase);
-    const int fm = (!claim_only && w.match) ? __ffs(w.match) - 1 : kGroup;
-    uint32_t empty = w.empty;
-    if (fm < kGroup && (!empty || fm < __ffs(empty) - 1)) {
+                            int64_t base, int64_t left, Window w0, bool claim_only, int gl,
+                            int gbase) {
+  for (const int64_t left0 = left; left > 0; left -= G) {
+    const Window w = left == left0 ? w0 : read_window<G>(a, base, left, code, tag, gl, gbase);
+    const int fm = (!claim_only && w.match) ? first_bit(w.match) : G;
+    if (fm < G && (!w.empty || fm < first_bit(w.empty))) {
       int64_t s = base + fm;
       if (s >= a.cap) s -= a.cap;
-      group_copy(a, a.table + s * a.stride + 16, value, gl);
+      group_copy<G>(a, a.table + s * a.stride + 16, value, gl);
       return 0;
     }
-    while (empty) {  // claim the first free slot; a lost race just marks that slot taken
-      const int e = __ffs(empty) - 1;
-      int64_t s = base + e;
-      if (s >= a.cap) s -= a.cap;
-      unsigned long long old = 0;
-      if (gl == e)
-        old = atomicCAS(reinterpret_cast<unsigned long long*>(state_ptr(a, s)), kStateEmpty, tag);
-      const bool won = __shfl(old == kStateEmpty ? 1 : 0, gbase + e) != 0;
-      if (won) {
-        if (gl == e) *reinterpret_cast<uint64_t*>(a.table + s * a.stride) = code;
-        group_copy(a, a.table + s * a.stride + 16, value, gl);
-        return 1;
-      }
-      empty &= ~(1u << e);
+    const int64_t s = claim_in_window(a, code, tag, base, w.empty, gl, gbase);
+    if (s >= 0) {
+      group_copy<G>(a, a.table + s * a.stride + 16, value, gl);
+      return 1;
     }
-    base += kGroup;
+    base += G;
     if (base >= a.cap) base -= a.cap;
   }
   return -1;
 }
 
-// A decode step (T == 1): item i is partition i; 8 lanes per item.
-__global__ __launch_bounds__(256) void store_step_kernel(StoreArgs a) {
+// A decode step (T == 1): item i is partition i, kStepGroup lanes per item. Everything that does
+// not depend on the table is loaded up front (both codes, the item's value row when it fits one
+// 16-byte piece per lane); the query's first window is read as whole slots when they are small
+// enough (`spec`), so a hit needs no further read; after the windows only a claim (one CAS)
+// is still a round trip. The query is answered before the key touches the table: a hit's value
+// is stored to `out` (its load complete) before any store into the table is issued.
+__global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t i = gid / kGroup;
-  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
+  constexpr int G = kStepGroup;
+  const int64_t i = gid / G;
+  const int lane = threadIdx.x & 63, gl = lane % G, gbase = lane - gl;
   if (i >= a.n) return;  // whole groups only: n is a count of items, groups are aligned
   const uint64_t tag = static_cast<uint64_t>(a.g0 + i) + 2;
+  const bool has_q = a.qc != nullptr;
   const uint64_t kcode = code_at(a.kc, a.code_bytes, i);
+  const uint64_t qcode = has_q ? code_at(a.qc, a.code_bytes, i) : 0;
+  const uint8_t* vrow = a.values + i * a.vbytes;
+  u32x4 vin = {0u, 0u, 0u, 0u};  // piece gl of the item's value row (`pre`)
+  if (a.pre && gl < a.pieces) vin = *reinterpret_cast<const u32x4*>(vrow + 16 * gl);
   const int64_t khome = home_slot(kcode, tag - 2, a.cap);
-  const uint64_t qcode = a.qc != nullptr ? code_at(a.qc, a.code_bytes, i) : 0;
-  const int64_t qhome = a.qc != nullptr ? home_slot(qcode, tag - 2, a.cap) : 0;
-  // the two first windows are independent: both reads are in flight together
-  const Window wk = read_window(a, khome, a.cap, kcode, tag, gl, gbase);
-  const Window wq = a.qc != nullptr ? read_window(a, qhome, a.cap, qcode, tag, gl, gbase)
-                                    : Window{0u, 0u};
-  if (a.qc != nullptr) {
-    const int64_t s = group_lookup(a, qcode, tag, qhome, wq, gl, gbase);
-    group_copy(a, a.out + i * a.vbytes, s >= 0 ? a.table + s * a.stride + 16 : nullptr, gl);
+  const int64_t qhome = has_q ? home_slot(qcode, tag - 2, a.cap) : 0;
+  // the two first windows are independent: their reads are in flight together
+  const Window wk = read_window<G>(a, khome, a.cap, kcode, tag, gl, gbase);
+  u32x4 qval[kSpecPieces];
+  Window wq{0u, 0u};
+  if (has_q)
+    wq = a.spec ? read_window_slots<G>(a, qhome, qcode, tag, gl, gbase, qval)
+                : read_window<G>(a, qhome, a.cap, qcode, tag, gl, gbase);
+
+  if (has_q) {
+    uint8_t* dst = a.out + i * a.vbytes;
+    const int fm = wq.match ? first_bit(wq.match) : G;
+    const int fe = wq.empty ? first_bit(wq.empty) : G;
+    if (fm < fe && a.spec) {
+      if (gl == fm) {
+#pragma unroll
+        for (int k = 0; k < kSpecPieces; ++k)
+          if (k < a.pieces) *reinterpret_cast<u32x4*>(dst + 16 * k) = qval[k];
+      }
+    } else {
+      const int64_t s = group_lookup<G>(a, qcode, tag, qhome, a.cap, wq, gl, gbase);
+      group_copy<G>(a, dst, s >= 0 ? a.table + s * a.stride + 16 : nullptr, gl);
+    }
   }
-  const int r = group_insert(a, kcode, tag, a.values + i * a.vbytes, khome, wk, false, gl, gbase);
+
+  int r;
+  const int fmk = wk.match ? first_bit(wk.match) : G;
+  int64_t s = -1;
+  if (fmk < G && (!wk.empty || fmk < first_bit(wk.empty))) {
+    s = khome + fmk;  // the partition's entry: overwrite its value
+    if (s >= a.cap) s -= a.cap;
+    r = 0;
+  } else {
+    s = claim_in_window(a, kcode, tag, khome, wk.empty, gl, gbase);
+    r = 1;
+  }
+  if (s >= 0) {
+    uint8_t* dst = a.table + s * a.stride + 16;
+    if (a.pre) {
+      if (gl < a.pieces) *reinterpret_cast<u32x4*>(dst + 16 * gl) = vin;
+    } else {
+      group_copy<G>(a, dst, vrow, gl);
+    }
+  } else {  // the first window had no room left: probe on
+    int64_t b = khome + G;
+    if (b >= a.cap) b -= a.cap;
+    const int64_t left = a.cap - G;
+    r = left > 0 ? group_insert<G>(a, kcode, tag, vrow, b, left,
+                                   read_window<G>(a, b, left, kcode, tag, gl, gbase), false, gl,
+                                   gbase)
+                 : -1;
+  }
   if (gl == 0) {
     if (r > 0) atomicAdd(&a.counts[a.g0 + i], 1ull);
     if (r < 0) atomicOr(a.full, 1);
@@ -262,13 +374,13 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
       const int j = src_in[o];
       uint8_t* dst = a.out + (first + o) * a.vbytes;
       if (j >= 0) {
-        group_copy(a, dst, a.values + (first + j) * a.vbytes, gl);
+        group_copy<kGroup>(a, dst, a.values + (first + j) * a.vbytes, gl);
       } else {
         const uint64_t c = code_at(a.qc, a.code_bytes, first + o);
         const int64_t h = home_slot(c, tag - 2, a.cap);
-        const int64_t sl = group_lookup(a, c, tag, h, read_window(a, h, a.cap, c, tag, gl, gbase),
-                                        gl, gbase);
-        group_copy(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, gl);
+        const int64_t sl = group_lookup<kGroup>(a, c, tag, h, a.cap,
+                                        read_window<kGroup>(a, h, a.cap, c, tag, gl, gbase), gl, gbase);
+        group_copy<kGroup>(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, gl);
       }
     }
   }
@@ -280,10 +392,10 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
     if (!klast[o]) continue;
     const uint64_t c = code_at(a.kc, a.code_bytes, first + o);
     const int64_t h = home_slot(c, tag - 2, a.cap);
-    const int64_t sl = group_lookup(a, c, tag, h, read_window(a, h, a.cap, c, tag, gl, gbase),
-                                    gl, gbase);
+    const int64_t sl = group_lookup<kGroup>(a, c, tag, h, a.cap,
+                                    read_window<kGroup>(a, h, a.cap, c, tag, gl, gbase), gl, gbase);
     if (sl >= 0)
-      group_copy(a, a.table + sl * a.stride + 16, a.values + (first + o) * a.vbytes, gl);
+      group_copy<kGroup>(a, a.table + sl * a.stride + 16, a.values + (first + o) * a.vbytes, gl);
     else if (gl == 0)
       klast[o] = 2;
   }
@@ -293,8 +405,8 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
     if (klast[o] != 2) continue;
     const uint64_t c = code_at(a.kc, a.code_bytes, first + o);
     const int64_t h = home_slot(c, tag - 2, a.cap);
-    const int r = group_insert(a, c, tag, a.values + (first + o) * a.vbytes, h,
-                               read_window(a, h, a.cap, c, tag, gl, gbase), true, gl, gbase);
+    const int r = group_insert<kGroup>(a, c, tag, a.values + (first + o) * a.vbytes, h, a.cap,
+                               read_window<kGroup>(a, h, a.cap, c, tag, gl, gbase), true, gl, gbase);
     if (r > 0) ++added;
     if (r < 0 && gl == 0) atomicOr(a.full, 1);
   }
@@ -345,13 +457,16 @@ extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, con
   const bool p16 = vbytes % 16 == 0 && aligned(table, 16) && aligned(values, 16) &&
                    (out == nullptr || aligned(out, 16));
   a.piece = p16 ? 16 : 8;
+  a.pieces = static_cast<int32_t>(vbytes / a.piece);
+  a.pre = p16 && a.pieces <= kStepGroup;
+  a.spec = p16 && a.pieces <= kSpecPieces;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = n / T;
   if (T == 1) {
-    const int64_t threads = n * kGroup;
-    const int64_t grid = (threads + 255) / 256;
+    const int64_t threads = n * kStepGroup;
+    const int64_t grid = (threads + kStepBlock - 1) / kStepBlock;
     LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many items (%lld)", (long long)n);
-    store_step_kernel<<<dim3(grid), dim3(256), 0, st>>>(a);
+    store_step_kernel<<<dim3(grid), dim3(kStepBlock), 0, st>>>(a);
     return launch_status("store_step_kernel");
   }
   LEMA_REQUIRE(P < (int64_t(1) << 31), "too many partitions (%lld)", (long long)P);
