@@ -1,0 +1,255 @@
+"""The LEMA transformer on MI355X: the reference's `ModelConfig` / `Transformer`
+(code/lema/model.py) for an all-LEMA model in hard mode, the configuration in which the
+exact op runs and a retrieval cache can be attached.
+
+Pre-RMSNorm, SwiGLU MLP, untied head, no biases, no positional encoding
+(code/lema/model.py:1-9). The projections, MLP and head are bf16 (or fp32) GEMMs on the
+matrix cores through torch; the attention of every block is the exact op of this package
+(sign-pack, latest-match resolve and gather in HIP), and a cached forward exchanges each
+layer's codes against the HBM store with no host round trip.
+
+Parameters are created and initialised in the reference's module order (embedding, then per
+block norm1, q, k, v, o, norm2, gate, up, down, then norm_f, lm_head; Gaussian std
+1/sqrt(fan_in) for every Linear and 1/sqrt(dim) for the embedding, the two residual-branch
+outputs scaled by 1/sqrt(2 * depth): code/lema/model.py:258-281), so the same seed gives the
+same weights.
+
+Only the hard (exact) op is implemented: the training surrogate (stick-breaking relaxation,
+straight-through binarization) and the softmax / gated-deltanet baselines are not part of the
+exact-match path.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .attention import code_dtype_for, lema_hard, pack_codes
+
+__all__ = ["ModelConfig", "SwiGLU", "Attention", "Block", "Transformer", "lm_loss"]
+
+ATTN_KINDS = ("lema",)
+POS_KINDS = ("nope",)
+
+
+def _pad128(n) -> int:
+    return -(-int(n) // 128) * 128
+
+
+@dataclass
+class ModelConfig:
+    """Geometry of a LEMA model (code/lema/model.py:33-82). `d_qk`, `d_v` default to
+    dim // num_heads, `dim_ff` to 8 * dim / 3; `vocab_size` and `dim_ff` are rounded up to a
+    multiple of 128 (the padded vocabulary rows are never targets)."""
+    vocab_size: int
+    depth: int
+    dim: int
+    num_heads: int
+    d_qk: int = 0
+    d_v: int = 0
+    dim_ff: int = 0
+    num_kv_heads: int = 0
+    attn: str = "lema"
+    pos: str = "nope"
+    rope_base: float = 10000.0
+    gdn_expand_v: int = 2
+    norm_eps: float = 1e-5
+
+    def __post_init__(self):
+        if self.attn not in ATTN_KINDS:
+            raise ValueError(f"attn must be one of {ATTN_KINDS} (the exact-match path), "
+                             f"got {self.attn!r}")
+        if self.pos not in POS_KINDS:
+            raise ValueError(f"pos must be one of {POS_KINDS}, got {self.pos!r}")
+        if (not self.d_qk or not self.d_v) and self.dim % self.num_heads:
+            raise ValueError(f"dim {self.dim} is not divisible by num_heads {self.num_heads}")
+        head = self.dim // self.num_heads
+        self.d_qk = self.d_qk or head
+        self.d_v = self.d_v or head
+        self.dim_ff = _pad128(self.dim_ff or 8 * self.dim / 3)
+        self.vocab_size = _pad128(self.vocab_size)
+        self.num_kv_heads = self.num_kv_heads or self.num_heads
+        if self.num_kv_heads != self.num_heads:
+            raise ValueError("grouped-query attention (num_kv_heads < num_heads) is "
+                             "implemented for softmax attention only")
+        if self.d_qk > 64:
+            raise ValueError(f"d_qk {self.d_qk} > 64: codes must pack into one uint64")
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "ModelConfig":
+        names = {f.name for f in dataclasses.fields(cls)}
+        return cls(**{k: v for k, v in d.items() if k in names})
+
+    def summary(self) -> str:
+        return (f"{self.depth}L d{self.dim} h{self.num_heads} d_qk {self.d_qk} d_v {self.d_v} "
+                f"dim_ff {self.dim_ff} attn {self.attn} pos {self.pos}")
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, dim: int, dim_ff: int):
+        super().__init__()
+        self.gate = nn.Linear(dim, dim_ff, bias=False)
+        self.up = nn.Linear(dim, dim_ff, bias=False)
+        self.down = nn.Linear(dim_ff, dim, bias=False)
+
+    def forward(self, x):
+        return self.down(F.silu(self.gate(x)) * self.up(x))
+
+
+class Attention(nn.Module):
+    """A LEMA attention block (code/lema/model.py:143-210): q, k, v projections viewed as
+    `[B, H, T, d]` (transposed views, read in place by the kernels), the exact op, o_proj."""
+
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.kind = cfg.attn
+        self.inner = None
+        self.q_proj = nn.Linear(cfg.dim, cfg.num_heads * cfg.d_qk, bias=False)
+        self.k_proj = nn.Linear(cfg.dim, cfg.num_kv_heads * cfg.d_qk, bias=False)
+        self.v_proj = nn.Linear(cfg.dim, cfg.num_kv_heads * cfg.d_v, bias=False)
+        self.o_proj = nn.Linear(cfg.num_heads * cfg.d_v, cfg.dim, bias=False)
+        self.alpha, self.cap, self.c, self.beta = 1.0, 2.0, 0.0, 2.0
+        self.hard = False
+        self.exact_fwd = False
+
+    def project(self, x):
+        """`[B, T, dim]` -> query and key pre-activations and values, `[B, H, T, d]`."""
+        B, T, _ = x.shape
+        c = self.cfg
+        zq = self.q_proj(x).view(B, T, c.num_heads, c.d_qk).transpose(1, 2)
+        zk = self.k_proj(x).view(B, T, c.num_kv_heads, c.d_qk).transpose(1, 2)
+        v = self.v_proj(x).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
+        return zq, zk, v
+
+    def merge(self, y):
+        B, _, T, _ = y.shape
+        return self.o_proj(y.transpose(1, 2).reshape(B, T, -1))
+
+    def forward(self, x):
+        if not self.hard:
+            raise NotImplementedError("only the exact (hard) op is implemented: call "
+                                      "model.set_hard(True)")
+        zq, zk, v = self.project(x)
+        return self.merge(lema_hard(zq, zk, v))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.norm1 = nn.RMSNorm(cfg.dim, eps=cfg.norm_eps)
+        self.attn = Attention(cfg)
+        self.norm2 = nn.RMSNorm(cfg.dim, eps=cfg.norm_eps)
+        self.mlp = SwiGLU(cfg.dim, cfg.dim_ff)
+        self.seg = None
+
+    def gpu_pre(self, x):
+        """Normalise, project, pack both codes (code/lema/model.py:224-227)."""
+        zq, zk, v = self.attn.project(self.norm1(x))
+        ct = code_dtype_for(self.attn.cfg.d_qk)
+        return pack_codes(zq, ct), pack_codes(zk, ct), v
+
+    def gpu_post(self, x, got):
+        """Merge the retrieved values and finish the layer (code/lema/model.py:229-232)."""
+        x = x + self.attn.merge(got)
+        return x + self.mlp(self.norm2(x))
+
+    def forward(self, x, store=None):
+        if store is not None:
+            pre, post = self.seg or (self.gpu_pre, self.gpu_post)
+            qc, kc, v = pre(x)
+            return post(x, store.exchange(qc, kc, v))
+        x = x + self.attn(self.norm1(x))
+        return x + self.mlp(self.norm2(x))
+
+
+class Transformer(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.tok_emb = nn.Embedding(cfg.vocab_size, cfg.dim)
+        self.blocks = nn.ModuleList(Block(cfg) for _ in range(cfg.depth))
+        self.norm_f = nn.RMSNorm(cfg.dim, eps=cfg.norm_eps)
+        self.lm_head = nn.Linear(cfg.dim, cfg.vocab_size, bias=False)
+        self.checkpoint_blocks = False
+        self._init_weights()
+
+    def _init_weights(self):
+        for m in self.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.normal_(m.weight, mean=0.0, std=1.0 / math.sqrt(m.weight.shape[1]))
+            elif isinstance(m, nn.Embedding):
+                nn.init.normal_(m.weight, mean=0.0, std=1.0 / math.sqrt(self.cfg.dim))
+        for b in self.blocks:
+            for lin in (b.attn.o_proj, b.mlp.down):
+                lin.weight.data.mul_(1.0 / math.sqrt(2 * self.cfg.depth))
+
+    def lema_layers(self):
+        return [b.attn for b in self.blocks if b.attn.kind == "lema"]
+
+    def set_hard(self, hard: bool = True):
+        for att in self.lema_layers():
+            att.hard = hard
+
+    def new_cache(self, place: str = "hbm", **kw):
+        """A retrieval cache for this model in device memory (the reference's host-RAM cache,
+        code/lema/model.py:306-324, moved to HBM): `max_cache_len=` or `capacity=` slots,
+        `batch=`, `max_load=`, `codes_hook=` as in `LemaCache`."""
+        from .cache import LemaCache
+        if place not in ("hbm", "vram"):
+            raise ValueError(f"a LEMA cache here lives in device memory (place='hbm'); "
+                             f"place={place!r} is not an implementation of it")
+        p = next(self.parameters())
+        kw.setdefault("dtype", p.dtype)
+        kw.pop("pin", None)
+        return LemaCache(self.cfg, device=p.device, **kw)
+
+    def forward(self, idx, *, cache=None, return_logits=True):
+        """Run `idx` through the model (code/lema/model.py:337-363).
+
+            forward(x)                                batched, no state
+            forward(x, cache=c, return_logits=False)  prefill: fills c, no logits
+            forward(next, cache=c)                    extending c
+
+        With a cache, queries match keys from before this call too, so a sequence can be fed
+        in pieces; any chunking gives the one-shot result.
+        """
+        if cache is not None and not (self.lema_layers()
+                                      and all(a.hard for a in self.lema_layers())):
+            raise ValueError("a cache needs an all-LEMA model in hard mode")
+        x = self.tok_emb(idx)
+        for li, blk in enumerate(self.blocks):
+            x = blk(x, store=(cache.layer(li) if cache is not None else None))
+        if cache is not None:
+            cache.t += idx.shape[-1]
+        return self.lm_head(self.norm_f(x)) if return_logits else None
+
+    def hidden(self, idx):
+        """The final normalised hidden states (the input of lm_head), without a cache."""
+        x = self.tok_emb(idx)
+        for blk in self.blocks:
+            x = blk(x)
+        return self.norm_f(x)
+
+    def n_params(self, embedding: bool = True) -> int:
+        n = sum(p.numel() for p in self.parameters())
+        if not embedding:
+            n -= self.tok_emb.weight.numel() + self.lm_head.weight.numel()
+        return n
+
+
+def lm_loss(model: Transformer, x: torch.Tensor, y: torch.Tensor, chunk: int = 1024):
+    """Mean next-token cross-entropy without holding the full `[B, T, vocab]` logits: the
+    head and the loss run `chunk` positions at a time on the final hidden states, in fp32
+    (code/lema/train.py:131-152, forward only)."""
+    h = model.hidden(x)
+    total = torch.zeros((), dtype=torch.float32, device=h.device)
+    for a in range(0, x.shape[1], chunk):
+        logits = model.lm_head(h[:, a:a + chunk])
+        total += F.cross_entropy(logits.float().flatten(0, 1), y[:, a:a + chunk].flatten(),
+                                 reduction="sum")
+    return total / y.numel()

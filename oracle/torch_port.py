@@ -6,7 +6,8 @@ stable argsorts order the 2T events by (code, position, query before key), a cum
 maximum of key positions runs inside each code's segment, and a scatter sends the answers
 back to query positions -- so timing it on the host's cores times the reference's own
 algorithm. `lema_hard_codes` adds the gather and mask of attention.py:157-158. Both run
-on CPU tensors with torch's intra-op threads.
+on the tensors' device (the CPU baseline times them on the host's cores; the model checker
+runs them on the GPU).
 """
 from __future__ import annotations
 
@@ -16,8 +17,10 @@ import torch
 def latest_prev_match_sorted(qc: torch.Tensor, kc: torch.Tensor) -> torch.Tensor:
     N, T = qc.shape
     codes = torch.cat([qc, kc], dim=1)                                  # [N, 2T] events
-    pos = torch.arange(T).repeat(2)
-    kind = torch.cat([torch.zeros(T, dtype=torch.long), torch.ones(T, dtype=torch.long)])
+    dev = qc.device
+    pos = torch.arange(T, device=dev).repeat(2)
+    kind = torch.cat([torch.zeros(T, dtype=torch.long, device=dev),
+                      torch.ones(T, dtype=torch.long, device=dev)])
     # stable sort by the secondary key (position, then query before key), then by code
     by_pos = (2 * pos + kind).expand(N, -1).argsort(dim=1, stable=True)
     by_code = codes.gather(1, by_pos).argsort(dim=1, stable=True)

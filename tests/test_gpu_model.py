@@ -1,0 +1,103 @@
+"""The LEMA model on the GPU: the exact op inside the model, the HBM cache in any chunking,
+the single-graph decoder, and the forward loss against the functional oracle model
+(code/tests/test_gpu.py:68-90 and 117-141; SURVEY C5 tolerance: loss within 1e-2 relative)."""
+import pytest
+import torch
+
+from oracle import torch_model
+from latest_exact_match_attention_amd.decode import decoder, worst_case_codes
+from latest_exact_match_attention_amd.model import ModelConfig, Transformer, lm_loss
+
+pytestmark = pytest.mark.gpu
+
+
+def make(dev, dtype=torch.float32, seed=0, **geo):
+    cfg = ModelConfig(**geo)
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        m = Transformer(cfg)
+    m = m.to(dtype).eval().requires_grad_(False)
+    m.set_hard(True)
+    return m, cfg
+
+
+GEOS = {"d64": dict(vocab_size=256, depth=2, dim=128, num_heads=1, d_qk=64, d_v=64),
+        "d4": dict(vocab_size=64, depth=2, dim=128, num_heads=2, d_qk=4, d_v=64)}
+
+
+@pytest.mark.parametrize("geo", list(GEOS))
+def test_store_chunked_equals_dense(dev, geo):
+    """Fed through the HBM cache whole, in chunks of 16 or token by token, the model gives
+    the dense forward (fp32; argmax agreement 1.0 as in the reference test)."""
+    m, cfg = make(dev, **GEOS[geo])
+    x = torch.randint(0, 64, (2, 96), device=dev)
+    with torch.no_grad():
+        dense = m(x)
+        for step in (x.shape[1], 16, 1):
+            cache = m.new_cache("hbm", max_cache_len=x.shape[1], batch=2)
+            parts = [m(x[:, s:s + step], cache=cache) for s in range(0, x.shape[1], step)]
+            chunked = torch.cat(parts, dim=1)
+            assert (dense.argmax(-1) == chunked.argmax(-1)).all(), step
+            assert (dense - chunked).abs().max() <= 1e-4 * dense.abs().max(), step
+            assert cache.entries() == int(cache.counts().sum()) > 0
+            assert cache.t == x.shape[1]
+
+
+def test_graph_decoder_reproduces_eager(dev):
+    m, cfg = make(dev, **GEOS["d4"])
+    prompt = torch.randint(0, 64, (2, 8), device=dev)
+    toks = []
+    with torch.no_grad():
+        for use_graph in (False, True):
+            c = m.new_cache("hbm", max_cache_len=64, batch=2)
+            m(prompt[:, :-1], cache=c, return_logits=False)
+            if use_graph:
+                before = c.store.table.clone(), c.entries()
+                d = decoder(m, c, tok=prompt[:, -1:])
+                assert torch.equal(c.store.table, before[0])   # warm-up left the table alone
+                assert c.entries() == before[1]
+                toks.append(torch.cat([d.step().clone() for _ in range(40)], dim=1))
+            else:
+                t, out = prompt[:, -1:], []
+                for _ in range(40):
+                    t = m(t, cache=c)[:, -1:].argmax(-1)
+                    out.append(t)
+                toks.append(torch.cat(out, dim=1))
+        assert torch.equal(toks[0], toks[1])
+
+
+def test_graph_decoder_with_worst_case_codes(dev):
+    """The worst-case hook draws fresh codes inside the graph: every step adds one entry per
+    (layer, stream, head) partition, and the retrieved values are zeros (random 64-bit
+    codes never match)."""
+    m, cfg = make(dev, dtype=torch.bfloat16, **GEOS["d4"])
+    c = m.new_cache("hbm", max_cache_len=64, batch=3, codes_hook=worst_case_codes(cfg.depth))
+    d = decoder(m, c, tok=torch.zeros(3, 1, dtype=torch.long, device=dev))
+    for s in range(1, 11):
+        d.step()
+        assert c.entries() == s * cfg.depth * 3 * cfg.num_heads
+    assert (c.counts() == 10).all()
+
+
+def test_lm_loss_matches_oracle_model(dev):
+    """bf16 model: the loss through the HIP op equals the functional oracle's (same weights,
+    torch GEMMs, the reference's sort-based exact op) within 1e-2 relative, and every layer's
+    match indices agree where the layer inputs agree (they do: the gather is exact)."""
+    geo = dict(vocab_size=512, depth=3, dim=256, num_heads=8, dim_ff=512)
+    m, cfg = make(dev, dtype=torch.bfloat16, **geo)
+    tok = torch.randint(0, 512, (2, 1025), device=dev)
+    x, y = tok[:, :-1], tok[:, 1:]
+    with torch.no_grad():
+        ours = lm_loss(m, x, y, chunk=256).item()
+        rec = []
+        want = torch_model.loss(m.state_dict(), cfg, x, y, chunk=256, record=rec).item()
+        assert abs(ours - want) <= 1e-2 * abs(want), (ours, want)
+        # per-layer indices: recompute ours layer by layer from the same inputs
+        from latest_exact_match_attention_amd import lema_from_codes, pack_codes
+        h = m.tok_emb(x)
+        for i, blk in enumerate(m.blocks):
+            zq, zk, v = blk.attn.project(blk.norm1(h))
+            _, src = lema_from_codes(pack_codes(zq, torch.int32), pack_codes(zk, torch.int32),
+                                     v, return_src=True)
+            assert torch.equal(src.long().view_as(rec[i]), rec[i]), i
+            h = blk(h)
