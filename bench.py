@@ -22,6 +22,15 @@ own C++ store (code/lema/csrc/store.cpp, compiled into oracle/_ref/) runs the sa
 steps on the host's cores as the CPU baseline, and every step's outputs and the final counts
 must agree bit for bit.
 
+lm_forward: the full LEMA language model forward with its loss -- vocab 50304, 24 layers,
+d_model 1536, 64 heads (d_qk = d_v = 24, 24-bit codes), SwiGLU 6144, bf16, random init
+(torch.manual_seed(0)), B4 x T16384 uniform token ids. A step is one forward + chunked
+cross-entropy; `value` = tokens per second. The projections, MLP and head are bf16 GEMMs on
+the matrix cores (torch); each layer's exact op is the fused HIP kernel. `roofline` prices
+the step's GEMM FLOPs against the dense bf16 MFMA peak; `lema_kernel` gives the fused op's
+own HBM fraction at the layer shape. `cpu_baseline` runs the model forward restated in torch
+with the reference's sort-based exact op on the host's cores, fp32, on a short sample.
+
 One GPU only: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
@@ -37,6 +46,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+LM_CONFIG = dict(vocab_size=50304, depth=24, dim=1536, num_heads=64, dim_ff=6144)
 BYTES_PER_QUERY = 4 + 4 + 4 + 128 + 128
 
 
@@ -46,7 +57,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="zipf_prefill", choices=["zipf_prefill", "decode"])
+    ap.add_argument("--workload", default="zipf_prefill",
+                    choices=["zipf_prefill", "decode", "lm_forward"])
+    ap.add_argument("--lm-batch", type=int, default=4)
+    ap.add_argument("--lm-seq", type=int, default=16384)
+    ap.add_argument("--lm-cpu-tokens", type=int, default=512,
+                    help="tokens (batch 1) of the lm_forward CPU-baseline sample")
     ap.add_argument("--decode-prefill", type=int, default=262144,
                     help="keys prefilled per partition for the decode workload")
     ap.add_argument("--decode-steps", type=int, default=1024)
@@ -295,13 +311,137 @@ def bench_decode(a):
     }
 
 
+def lm_flops_per_token(cfg) -> float:
+    """Matrix-multiply FLOPs of one token's forward: q, k, v, o, gate, up, down per layer and
+    the head (2 FLOPs per multiply-add)."""
+    d, ff, H = cfg.dim, cfg.dim_ff, cfg.num_heads
+    per_layer = 2 * d * H * (2 * cfg.d_qk + cfg.d_v) + 2 * H * cfg.d_v * d + 6 * d * ff
+    return cfg.depth * per_layer + 2 * d * cfg.vocab_size
+
+
+def cpu_baseline_lm(model, cfg, tokens: int):
+    """The forward restated in torch with the reference's sort-based exact op
+    (oracle/torch_model.py), fp32 on the host's cores, batch 1 x `tokens`."""
+    import torch
+    from oracle import torch_model
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    sd = {k: v.float().cpu() for k, v in model.state_dict().items()}
+    g = torch.Generator().manual_seed(1)
+    tok = torch.randint(0, 50304, (1, tokens + 1), generator=g)
+    x, y = tok[:, :-1], tok[:, 1:]
+    times = []
+    with torch.no_grad():
+        torch_model.loss(sd, cfg, x, y)
+        t_end = time.perf_counter() + 20.0
+        while len(times) < 5 and (time.perf_counter() < t_end or len(times) < 2):
+            t0 = time.perf_counter()
+            torch_model.loss(sd, cfg, x, y)
+            times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": tokens / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"batch 1 x {tokens} tokens of the same model (fp32 weights), forward + "
+                      f"loss; median of {len(times)} runs, {med:.2f} s per run; per-token "
+                      f"cost grows with T only through the exact op's sort"}
+
+
+def bench_lm(a):
+    import torch
+    from latest_exact_match_attention_amd import build, pack_codes
+    from latest_exact_match_attention_amd.attention import launch_hard
+    from latest_exact_match_attention_amd.model import ModelConfig, Transformer, lm_loss
+
+    if not build.LIB.exists():
+        build.build()
+    cfg = ModelConfig(**LM_CONFIG)
+    B, T = a.lm_batch, a.lm_seq
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Transformer(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model.eval().requires_grad_(False)
+    model.set_hard(True)
+    g = torch.Generator().manual_seed(0)
+    tok = torch.randint(0, 50304, (B, T + 1), generator=g).to(dev)
+    x, y = tok[:, :-1], tok[:, 1:]
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        for _ in range(a.warmup):
+            loss = lm_loss(model, x, y)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(a.steps):
+            loss = lm_loss(model, x, y)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / a.steps
+        # the fused exact op alone at the layer shape (layer 0's codes and values)
+        blk = model.blocks[0]
+        zq, zk, v = blk.attn.project(blk.norm1(model.tok_emb(x)))
+        qc = pack_codes(zq, torch.int32).view(B * cfg.num_heads, T)
+        kc = pack_codes(zk, torch.int32).view(B * cfg.num_heads, T)
+        yv = torch.empty_like(v)
+        for _ in range(3):
+            launch_hard(qc, kc, v, yv)
+        torch.cuda.synchronize()
+        n_l = 20
+        e0.record(stream)
+        for _ in range(n_l):
+            launch_hard(qc, kc, v, yv)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_l = e0.elapsed_time(e1) / n_l
+        src = torch.empty((B, cfg.num_heads, T), dtype=torch.int32, device=dev)
+        launch_hard(qc, kc, v, yv, src)
+        hits = float((src >= 0).float().mean())
+    ntok = B * T
+    flops = lm_flops_per_token(cfg) * ntok
+    tflops = flops / (ms * 1e-3) / 1e12
+    nq = B * cfg.num_heads * T
+    bpq = 4 + 4 + 4 + 2 * 2 * cfg.d_v
+    gbs = bpq * nq / (ms_l * 1e-3) / 1e9
+    cpu = None if a.no_cpu_baseline else cpu_baseline_lm(model, cfg, a.lm_cpu_tokens)
+    return {
+        "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
+        "value": ntok / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 (GEMMs fp32-accumulated), int32 codes",
+        "data": "synthetic (uniform token ids, seed 0; random-init weights, seed 0)",
+        "config": {"workload": "lm_forward", "model": cfg.summary(), "vocab": cfg.vocab_size,
+                   "global_batch": B, "seq_len": T, "loss": float(loss),
+                   "layer0_hit_rate": round(hits, 4), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tflops / MFMA_BF16_PEAK_TFLOPS,
+                     "traffic": None, "kernel": "whole forward (GEMM FLOPs / step time)",
+                     "flops_per_token": lm_flops_per_token(cfg)},
+        "lema_kernel": {"kernel": "resolve_kernel (fused resolve + gather), one layer",
+                        "us": ms_l * 1e3, "queries": nq, "bytes_per_query": bpq,
+                        "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS},
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got "
               f"--gpus {a.gpus}", file=sys.stderr)
         return 2
-    out = bench_decode(a) if a.workload == "decode" else bench_prefill(a)
+    run = {"decode": bench_decode, "lm_forward": bench_lm}.get(a.workload, bench_prefill)
+    out = run(a)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -249,7 +249,10 @@ def lm_loss(model: Transformer, x: torch.Tensor, y: torch.Tensor, chunk: int = 1
     h = model.hidden(x)
     total = torch.zeros((), dtype=torch.float32, device=h.device)
     for a in range(0, x.shape[1], chunk):
-        logits = model.lm_head(h[:, a:a + chunk])
-        total += F.cross_entropy(logits.float().flatten(0, 1), y[:, a:a + chunk].flatten(),
+        # a contiguous 2-D block: the head is then one plain GEMM (a strided 3-D slice would
+        # make matmul broadcast the transposed weight into a batched product instead)
+        hc = h[:, a:a + chunk].reshape(-1, h.shape[-1]).contiguous()
+        logits = model.lm_head(hc)
+        total += F.cross_entropy(logits.float(), y[:, a:a + chunk].reshape(-1),
                                  reduction="sum")
     return total / y.numel()

@@ -61,7 +61,8 @@ def loss(sd: dict, cfg, x: torch.Tensor, y: torch.Tensor, chunk: int = 1024, rec
     h = forward_hidden(sd, cfg, x, record)
     total = torch.zeros((), dtype=torch.float32, device=h.device)
     for a in range(0, x.shape[1], chunk):
-        logits = F.linear(h[:, a:a + chunk], sd["lm_head.weight"])
-        total += F.cross_entropy(logits.float().flatten(0, 1), y[:, a:a + chunk].flatten(),
+        hc = h[:, a:a + chunk].reshape(-1, h.shape[-1]).contiguous()   # 2-D: a plain GEMM
+        logits = F.linear(hc, sd["lm_head.weight"])
+        total += F.cross_entropy(logits.float(), y[:, a:a + chunk].reshape(-1),
                                  reduction="sum")
     return total / y.numel()

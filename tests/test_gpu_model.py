@@ -101,3 +101,39 @@ def test_lm_loss_matches_oracle_model(dev):
                                      v, return_src=True)
             assert torch.equal(src.long().view_as(rec[i]), rec[i]), i
             h = blk(h)
+
+
+def test_full_lm_forward_loss_matches_oracle(dev):
+    """The full language-model configuration (vocab 50304, 24 layers, d 1536, 64 heads of
+    24-bit codes, SwiGLU 6144, bf16, random init at seed 0) on B4 x T16384 uniform tokens:
+    loss within 1e-2 relative of the functional oracle model, and every layer's match
+    indices identical."""
+    geo = dict(vocab_size=50304, depth=24, dim=1536, num_heads=64, dim_ff=6144)
+    cfg = ModelConfig(**geo)
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            m = Transformer(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    m.eval().requires_grad_(False)
+    m.set_hard(True)
+    g = torch.Generator().manual_seed(0)
+    tok = torch.randint(0, 50304, (4, 16385), generator=g).to(dev)
+    x, y = tok[:, :-1], tok[:, 1:]
+    with torch.no_grad():
+        ours = lm_loss(m, x, y).item()
+        rec = []
+        want = torch_model.loss(m.state_dict(), cfg, x, y, record=rec).item()
+        assert abs(ours - want) <= 1e-2 * abs(want), (ours, want)
+        from latest_exact_match_attention_amd import lema_from_codes, pack_codes
+        h = m.tok_emb(x)
+        for i, blk in enumerate(m.blocks):
+            zq, zk, v = blk.attn.project(blk.norm1(h))
+            _, src = lema_from_codes(pack_codes(zq, torch.int32), pack_codes(zk, torch.int32),
+                                     v, return_src=True)
+            assert torch.equal(src.long().view_as(rec[i]), rec[i]), i
+            h = blk(h)
+    print(f"full LM loss {ours:.6f} (oracle {want:.6f})", flush=True)

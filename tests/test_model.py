@@ -116,3 +116,29 @@ def test_model_oracle_zero_qk_is_previous_token_copy():
             @ sd[p + "mlp.down.weight"].T
     want = F.rms_norm(x, (32,), sd["norm_f.weight"], cfg.norm_eps)
     assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def _aten_ops(fn):
+    from torch.profiler import ProfilerActivity, profile
+    with profile(activities=[ProfilerActivity.CPU]) as p:
+        fn()
+    return {e.key for e in p.key_averages()}
+
+
+def test_losses_run_the_head_as_plain_gemms():
+    """The chunked head must see 2-D contiguous blocks: a strided 3-D slice would make matmul
+    expand the transposed weight into a batched bf16 product (aten::bmm), a form that is
+    not used anywhere on this path."""
+    from latest_exact_match_attention_amd import model as M
+    cfg = ModelConfig(vocab_size=256, depth=1, dim=64, num_heads=2)
+    torch.manual_seed(0)
+    m = Transformer(cfg).to(torch.bfloat16)
+    x = torch.randint(0, 256, (2, 96))
+    y = torch.randint(0, 256, (2, 96))
+    h = torch.randn(2, 96, 64, dtype=torch.bfloat16)
+    m.hidden = lambda idx: h                      # the head and the loss alone
+    ops = _aten_ops(lambda: M.lm_loss(m, x, y, chunk=32))
+    assert "aten::mm" in ops and "aten::bmm" not in ops
+    sd = {k: v.float() for k, v in Transformer(cfg).state_dict().items()}
+    ops = _aten_ops(lambda: torch_model.loss(sd, cfg, x, y, chunk=32))
+    assert "aten::bmm" not in ops
