@@ -31,6 +31,16 @@ the step's GEMM FLOPs against the dense bf16 MFMA peak; `lema_kernel` gives the 
 own HBM fraction at the layer shape. `cpu_baseline` runs the model forward restated in torch
 with the reference's sort-based exact op on the host's cores, fp32, on a short sample.
 
+long_context: B1 H64, T = 2^24 fed through the HBM store in 16 calls of 2^20 positions
+(one `HashStore.exchange` per call, P = 64 partitions x T = 2^20), 32-bit codes: each key is
+uniform with probability 0.9, else a copy of the key d positions back, d ~ Geometric(1e-5)
+(mean 1e5); each query likewise copies an earlier key or is uniform; d_v 24 bf16 ~N(0,1).
+Codes come from a counter-based hash of (seed, head, position) and values from a per-call
+seeded generator, made on the device for each call before it is timed. `value` = queries
+per second over the timed exchanges. The first call also runs through the reference's own
+C++ store on the host (`--long-parity-calls` of them): outputs and counts must agree bit for
+bit, and its time is the CPU baseline.
+
 One GPU only: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
@@ -58,7 +68,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="zipf_prefill",
-                    choices=["zipf_prefill", "decode", "lm_forward"])
+                    choices=["zipf_prefill", "decode", "lm_forward", "long_context"])
+    ap.add_argument("--long-calls", type=int, default=16,
+                    help="calls of 2^20 positions of the long_context workload to run")
+    ap.add_argument("--long-parity-calls", type=int, default=1,
+                    help="leading calls also run through the reference store on the host")
     ap.add_argument("--lm-batch", type=int, default=4)
     ap.add_argument("--lm-seq", type=int, default=16384)
     ap.add_argument("--lm-cpu-tokens", type=int, default=512,
@@ -434,13 +448,114 @@ def bench_lm(a):
     }
 
 
+def bench_long(a):
+    import math
+    import torch
+    from latest_exact_match_attention_amd import build
+    from latest_exact_match_attention_amd.cache import HashStore
+    from latest_exact_match_attention_amd.workloads import LONG_CONTEXT, long_context_codes
+
+    if not build.LIB.exists():
+        build.build()
+    H, T, L, dv = LONG_CONTEXT["H"], LONG_CONTEXT["T"], LONG_CONTEXT["call"], LONG_CONTEXT["dv"]
+    calls = max(1, min(a.long_calls, T // L))
+    dev = torch.device("cuda", 0)
+    cap = math.ceil(H * T / 0.5)
+    store = HashStore(dv, groups=H, dtype=torch.bfloat16, capacity=cap, device=dev)
+    ref = None
+    n_par = 0 if a.no_cpu_baseline else max(0, min(a.long_parity_calls, calls))
+    if n_par:
+        import oracle
+        ref = oracle.ref_store()
+        if ref is None:
+            print("oracle/_ref/lema_store_ref.so missing: no CPU baseline", file=sys.stderr)
+            n_par = 0
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    if n_par:
+        cap_h = math.ceil(H * L * n_par / 0.5)
+        host_table = torch.zeros((cap_h, 16 + 2 * dv), dtype=torch.uint8)
+        host_counts = torch.zeros(H, dtype=torch.int64)
+    stream = torch.cuda.current_stream(dev)
+    total_ms, per_call, cpu_s, same = 0.0, [], [], True
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for c in range(calls):
+        qc64, kc64 = long_context_codes(0, H, c * L, (c + 1) * L, dev)
+        qc, kc = qc64.to(torch.int32).contiguous(), kc64.to(torch.int32).contiguous()
+        g = torch.Generator(device=dev).manual_seed(1000 + c)
+        v = torch.randn((H * L, dv), device=dev, generator=g).to(torch.bfloat16)
+        out = torch.empty_like(v)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        store.exchange(qc.view(-1), kc.view(-1), v, out, L, 0, check=False)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        store.check_full()
+        ms = e0.elapsed_time(e1)
+        total_ms += ms
+        per_call.append(round(ms, 3))
+        print(f"long_context call {c + 1}/{calls}: {ms:.2f} ms", file=sys.stderr, flush=True)
+        if c < n_par:
+            qh, kh = qc64.view(-1).cpu(), kc64.view(-1).cpu()
+            vh = v.view(torch.int16).cpu()
+            oh = torch.empty_like(vh)
+            t0 = time.perf_counter()
+            host_counts += ref.exchange(host_table, qh, kh, vh, oh, L, 0, cap_h, 2 * dv)
+            cpu_s.append(time.perf_counter() - t0)
+            same = same and bool(torch.equal(out.view(torch.int16).cpu(), oh))
+            print(f"  reference store: {cpu_s[-1]:.2f} s, outputs identical: {same}",
+                  file=sys.stderr, flush=True)
+        del qc64, kc64, qc, kc, v, out
+    nq = H * L * calls
+    bpq = 4 + 4 + 4 + 2 * 2 * dv
+    achieved = bpq * nq / (total_ms * 1e-3) / 1e9
+    cpu = None
+    parity = None
+    if n_par:
+        counts_same = bool(torch.equal(store.counts, host_counts)) if n_par == calls else None
+        parity = {"calls_checked": n_par, "outputs_identical": same,
+                  "counts_identical": counts_same}
+        cpu = {"value": H * L * n_par / sum(cpu_s), "unit": "queries/s", "cores": threads,
+               "kind": "reference",
+               "sample": f"the first {n_par} call(s) of 64 x 2^20 positions through "
+                         f"code/lema/csrc/store.cpp (compiled from source, OpenMP) on a host "
+                         f"table of {cap_h} slots; {sum(cpu_s):.2f} s"}
+        if not same:
+            print("long_context parity FAILED", file=sys.stderr)
+    return {
+        "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
+        "value": nq / (total_ms * 1e-3),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": calls,
+        "warmup": 0,
+        "ms_per_step": total_ms / calls,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32 codes (32-bit), bf16 values (opaque 48-byte rows)",
+        "data": "synthetic (counter-based hash codes, seed 0; per-call seeded N(0,1) values)",
+        "config": {"workload": "long_context", "B": 1, "H": H, "T": L * calls,
+                   "positions_per_call": L, "calls": calls, "d_v": dv, "capacity": cap,
+                   "table_bytes": cap * (16 + 2 * dv), "load_after": round(store.load(), 4),
+                   "ms_per_call": per_call, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "store exchange (all launches of a call)",
+                     "bytes_per_query": bpq, "queries_per_call": H * L},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+
+
 def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got "
               f"--gpus {a.gpus}", file=sys.stderr)
         return 2
-    run = {"decode": bench_decode, "lm_forward": bench_lm}.get(a.workload, bench_prefill)
+    run = {"decode": bench_decode, "lm_forward": bench_lm,
+           "long_context": bench_long}.get(a.workload, bench_prefill)
     out = run(a)
     print(json.dumps(out), flush=True)
     return 0
