@@ -63,6 +63,7 @@ class HashStore:
         self.table = torch.zeros((self.cap, self.stride), dtype=torch.uint8, device=self.device)
         self.counts_device = torch.zeros(groups, dtype=torch.int64, device=self.device)
         self.full_flag = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._ws = None          # scratch of long calls (bulk path), grown on demand
 
     @property
     def counts(self) -> torch.Tensor:
@@ -87,7 +88,8 @@ class HashStore:
         position order. Device tensors: codes int64 (or int32 for codes below 2^32), values and
         out rows of `vbytes` bytes in any dtype. `qcodes=None` only inserts. With `check` the
         full flag is read back (a device sync) and a full table raises like the reference;
-        without it, call `check_full()` later (e.g. after a graph replay)."""
+        without it, call `check_full()` later (e.g. after a graph replay). A long call (int32
+        codes, T > 2048) takes the bulk path with a device workspace this store keeps."""
         kc, cb = _codes(kcodes)
         n = kc.numel()
         if qcodes is not None:
@@ -113,13 +115,24 @@ class HashStore:
                 raise ValueError(f"out must be a contiguous buffer of {n} x {self.vbytes} bytes")
         if check:
             self.full_flag.zero_()
-        _lib.check(_lib.lib().lema_store_exchange(
+        L = _lib.lib()
+        ws_bytes = L.lema_store_workspace_bytes(n, T, cb)
+        ws = self._workspace(ws_bytes) if ws_bytes > 0 else None
+        _lib.check(L.lema_store_exchange_ws(
             self.table.data_ptr(), self.cap, self.vbytes,
             qc.data_ptr() if qc is not None else None, kc.data_ptr(), cb, values.data_ptr(),
             out.data_ptr() if qc is not None else None, n, T, g0,
-            self.counts_device.data_ptr(), self.full_flag.data_ptr(), _lib.stream_of(kc)))
+            self.counts_device.data_ptr(), self.full_flag.data_ptr(),
+            ws.data_ptr() if ws is not None else None, ws_bytes, _lib.stream_of(kc)))
         if check:
             self.check_full()
+
+    def _workspace(self, nbytes: int) -> torch.Tensor:
+        """Device scratch of a long call (kept for the next one; grown when too small)."""
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = None
+            self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self._ws
 
     def check_full(self):
         """Raise like the reference (code/lema/csrc/store.cpp:159-160) if some key since the

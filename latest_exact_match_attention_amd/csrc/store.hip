@@ -413,15 +413,360 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
   if (gl == 0 && added > 0) atomicAdd(&a.counts[a.g0 + p], static_cast<unsigned long long>(added));
 }
 
+// ------------------------------------------------------------------ bulk calls
+// A call with many positions per partition (32-bit codes) runs in sub-calls of up to kBulkSpan
+// positions, each as a few kernels over all of its items at once instead of one launch per
+// 1024-position sub-chunk:
+//   clear    the scratch group table;
+//   chunks   one workgroup per (partition, 1024-chunk): in-chunk answers of the queries (LDS
+//            resolver), the chunk's key summary (code -> latest position, the LDS table written
+//            out), and every distinct key code entered in the group table under
+//            (partition + 1) << 32 | code -- one 64-bit CAS, no half-written key -- with the
+//            chunk's bit in the code's 64-bit chunk mask and its latest position (atomicMax);
+//   queries  a query without an in-chunk answer takes the highest chunk below its own in its
+//            code's mask and that chunk's summary gives the key; with no such chunk it looks
+//            the store up (the table still holds exactly the keys before the sub-call);
+//   overwrite  every (partition, code) of the sub-call writes the value of its latest key over
+//            its existing store entry, or is marked;
+//   claim    marked codes claim store slots; a last pass counts the claims per partition.
+// The kernel boundaries order lookups before overwrites before claims, as the store needs.
+constexpr int kBulkSpan = 64 * kChunk;  // positions per sub-call: chunk masks fit 64 bits
+constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots, the sentinel's
+
+struct BulkWs {
+  uint64_t* gt_key;    // (partition + 1) << 32 | code, 0 = free
+  uint64_t* gt_mask;   // bit c: chunk c of the sub-call holds keys with this code
+  int32_t* gt_last;    // latest key position of the code in the sub-call
+  int32_t* gt_flag;    // 1: needs a store slot, 2: claimed one
+  uint32_t* sum_code;  // per (partition, chunk): the kSlots key-code slots
+  int32_t* sum_pos;    // per (partition, chunk): kSumPos latest positions
+  int32_t* src_in;     // per query of the sub-call: in-chunk answer (sub-call position) or -1
+  int64_t gt_cap;      // power of two
+  int32_t nch;         // chunks per partition in the sub-call
+};
+
+__device__ __forceinline__ int64_t gt_home(uint64_t key, int64_t cap) {
+  return static_cast<int64_t>(splitmix_fin(key) & static_cast<uint64_t>(cap - 1));
+}
+
+// Find or enter `key` in the group table (one thread); the table is at most half full.
+__device__ __forceinline__ int64_t gt_claim(const BulkWs& w, uint64_t key) {
+  int64_t sl = gt_home(key, w.gt_cap);
+  for (int64_t left = w.gt_cap; left > 0; --left) {
+    const uint64_t k = w.gt_key[sl];
+    if (k == key) return sl;
+    if (k == 0) {
+      const unsigned long long old =
+          atomicCAS(reinterpret_cast<unsigned long long*>(&w.gt_key[sl]), 0ull,
+                    static_cast<unsigned long long>(key));
+      if (old == 0 || old == key) return sl;
+    }
+    sl = (sl + 1) & (w.gt_cap - 1);
+  }
+  return -1;
+}
+
+// Slot of `key` in the group table or -1, kGroup lanes probing kGroup slots per read.
+__device__ __forceinline__ int64_t gt_find_group(const BulkWs& w, uint64_t key, int gl, int gbase) {
+  int64_t base = gt_home(key, w.gt_cap);
+  for (int64_t left = w.gt_cap; left > 0; left -= kGroup) {
+    const uint64_t k = w.gt_key[(base + gl) & (w.gt_cap - 1)];
+    const Window win = window_bits<kGroup>(k == key, k == 0, gbase);
+    const int fm = win.match ? first_bit(win.match) : kGroup;
+    const int fe = win.empty ? first_bit(win.empty) : kGroup;
+    if (fm < fe) return (base + fm) & (w.gt_cap - 1);
+    if (win.empty) return -1;
+    base = (base + kGroup) & (w.gt_cap - 1);
+  }
+  return -1;
+}
+
+// Latest position of `code` in a chunk summary (the code is known to be there), kGroup lanes
+// reading kGroup consecutive slots (two 4-slot buckets) per step.
+__device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int32_t* pos,
+                                                uint32_t code, int gl, int gbase) {
+  if (code == sentinel<uint32_t>()) return pos[kSlots];
+  int base = 4 * bucket_of<kBuckets>(fold(code));
+  for (int left = kSlots; left > 0; left -= kGroup) {
+    const uint32_t c = codes[(base + gl) & (kSlots - 1)];
+    const Window win = window_bits<kGroup>(c == code, c == sentinel<uint32_t>(), gbase);
+    const int fm = win.match ? first_bit(win.match) : kGroup;
+    const int fe = win.empty ? first_bit(win.empty) : kGroup;
+    if (fm < fe) return pos[(base + fm) & (kSlots - 1)];
+    if (win.empty) return -1;
+    base = (base + kGroup) & (kSlots - 1);
+  }
+  return -1;
+}
+
+__global__ __launch_bounds__(256) void bulk_clear_kernel(BulkWs w) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < w.gt_cap;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    w.gt_key[i] = 0;
+    w.gt_mask[i] = 0;
+    w.gt_last[i] = -1;
+    w.gt_flag[i] = 0;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkWs w) {
+  __shared__ ResolveLds<uint32_t> s;
+  const int64_t p = blockIdx.x / w.nch;
+  const int c = static_cast<int>(blockIdx.x - p * w.nch);
+  const int t = threadIdx.x;
+  const int64_t first = p * a.T + a.s0 + static_cast<int64_t>(c) * kChunk;
+  const int n = a.len - c * kChunk < kChunk ? a.len - c * kChunk : kChunk;
+  const uint32_t SENT = sentinel<uint32_t>();
+  const uint32_t* qc = static_cast<const uint32_t*>(a.qc);
+  const uint32_t* kc = static_cast<const uint32_t*>(a.kc);
+
+  // 1. in-chunk answers of the queries, as positions of the sub-call
+  if (qc != nullptr) {
+    ResolveArgs ra{};
+    ra.qc = qc + first;
+    ra.kc = kc + first;
+    ra.N = 1;
+    ra.T = n;
+    ra.nchunks = 1;
+    int32_t src[kPer];
+    resolve_chunk(s, ra, 0, 0, t, [] { __syncthreads(); }, src);
+    int32_t* out = w.src_in + p * a.len + static_cast<int64_t>(c) * kChunk;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int o = q * kThreads + t;
+      if (o < n) out[o] = src[q] >= 0 ? c * kChunk + src[q] : -1;
+    }
+  }
+  __syncthreads();
+
+  // 2. the chunk's key codes with their latest position
+  for (int x = t; x < kSlots; x += kThreads) s.code[x] = SENT;
+  for (int x = t; x <= kSlots; x += kThreads) s.pos[x] = -1;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int o = q * kThreads + t;
+    if (o >= n) continue;
+    const uint32_t code = kc[first + o];
+    int slot = kSlots;
+    if (code != SENT) {
+      bool ins;
+      slot = table_claim<uint32_t, kBuckets>(s.code, code, SENT, bucket_of<kBuckets>(fold(code)), ins);
+    }
+    atomicMax(&s.pos[slot], o);
+  }
+  __syncthreads();
+
+  // 3. the summary, and every distinct code into the group table
+  const int64_t sum = p * w.nch + c;
+  uint32_t* scode = w.sum_code + sum * kSlots;
+  int32_t* spos = w.sum_pos + sum * kSumPos;
+  for (int x = t; x < kSlots; x += kThreads) scode[x] = s.code[x];
+  for (int x = t; x <= kSlots; x += kThreads) {
+    const int32_t lp = s.pos[x];
+    spos[x] = lp;
+    if (lp < 0) continue;
+    const uint32_t code = x < kSlots ? s.code[x] : SENT;
+    const uint64_t key = (static_cast<uint64_t>(p + 1) << 32) | code;
+    const int64_t g = gt_claim(w, key);
+    if (g < 0) {  // cannot happen with the table at most half full; fail loudly
+      atomicOr(a.full, 2);
+      continue;
+    }
+    atomicOr(reinterpret_cast<unsigned long long*>(&w.gt_mask[g]), 1ull << c);
+    atomicMax(&w.gt_last[g], c * kChunk + lp);
+  }
+}
+
+__global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t i = gid / kGroup;  // query of the sub-call: partition i / len, position i % len
+  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
+  const int64_t n = static_cast<int64_t>(a.n / a.T) * a.len;
+  if (i >= n) return;
+  const int64_t p = i / a.len;
+  const int o = static_cast<int>(i - p * a.len);
+  const int64_t base = p * a.T + a.s0;  // item of the sub-call's position 0
+  uint8_t* dst = a.out + (base + o) * a.vbytes;
+  int32_t j = w.src_in[i];
+  if (j < 0) {
+    const uint32_t code = static_cast<const uint32_t*>(a.qc)[base + o];
+    const int c = o / kChunk;
+    const int64_t g = gt_find_group(w, (static_cast<uint64_t>(p + 1) << 32) | code, gl, gbase);
+    const uint64_t m = g >= 0 ? (w.gt_mask[g] & ((1ull << c) - 1)) : 0;
+    if (m) {
+      const int c2 = 63 - __clzll(m);
+      const int64_t sum = p * w.nch + c2;
+      const int32_t lp = summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code,
+                                      gl, gbase);
+      j = lp >= 0 ? c2 * kChunk + lp : -1;
+    }
+    if (j < 0) {
+      const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
+      const int64_t h = home_slot(code, tag - 2, a.cap);
+      const int64_t sl = group_lookup<kGroup>(
+          a, code, tag, h, a.cap, read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), gl, gbase);
+      group_copy<kGroup>(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, gl);
+      return;
+    }
+  }
+  group_copy<kGroup>(a, dst, a.values + (base + j) * a.vbytes, gl);
+}
+
+__global__ __launch_bounds__(256) void bulk_overwrite_kernel(StoreArgs a, BulkWs w) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t g = gid / kGroup;
+  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
+  if (g >= w.gt_cap) return;
+  const uint64_t key = w.gt_key[g];
+  if (key == 0) return;
+  const int64_t p = static_cast<int64_t>(key >> 32) - 1;
+  const uint64_t code = key & 0xFFFFFFFFull;
+  const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
+  const int64_t h = home_slot(code, tag - 2, a.cap);
+  const int64_t sl = group_lookup<kGroup>(
+      a, code, tag, h, a.cap, read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), gl, gbase);
+  if (sl >= 0) {
+    const uint8_t* v = a.values + (p * a.T + a.s0 + w.gt_last[g]) * a.vbytes;
+    group_copy<kGroup>(a, a.table + sl * a.stride + 16, v, gl);
+  } else if (gl == 0) {
+    w.gt_flag[g] = 1;
+  }
+}
+
+__global__ __launch_bounds__(256) void bulk_claim_kernel(StoreArgs a, BulkWs w) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t g = gid / kGroup;
+  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
+  if (g >= w.gt_cap || w.gt_flag[g] != 1) return;
+  const uint64_t key = w.gt_key[g];
+  const int64_t p = static_cast<int64_t>(key >> 32) - 1;
+  const uint64_t code = key & 0xFFFFFFFFull;
+  const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
+  const int64_t h = home_slot(code, tag - 2, a.cap);
+  const uint8_t* v = a.values + (p * a.T + a.s0 + w.gt_last[g]) * a.vbytes;
+  const int r = group_insert<kGroup>(a, code, tag, v, h, a.cap,
+                                     read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), true,
+                                     gl, gbase);
+  if (gl == 0) {
+    if (r > 0) w.gt_flag[g] = 2;
+    if (r < 0) atomicOr(a.full, 1);
+  }
+}
+
+// Claims per partition: a contiguous range of the group table per workgroup, counted in LDS
+// (up to kCountParts partitions) and added to counts once per partition and workgroup.
+constexpr int kCountParts = 4096;
+__global__ __launch_bounds__(256) void bulk_count_kernel(StoreArgs a, BulkWs w, int64_t span) {
+  __shared__ uint32_t hist[kCountParts];
+  const int64_t P = a.n / a.T;
+  const bool local = P <= kCountParts;
+  if (local)
+    for (int x = threadIdx.x; x < P; x += blockDim.x) hist[x] = 0;
+  __syncthreads();
+  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * span;
+  const int64_t g1 = g0 + span < w.gt_cap ? g0 + span : w.gt_cap;
+  for (int64_t g = g0 + threadIdx.x; g < g1; g += blockDim.x) {
+    if (w.gt_flag[g] != 2) continue;
+    const int64_t p = static_cast<int64_t>(w.gt_key[g] >> 32) - 1;
+    if (local)
+      atomicAdd(&hist[p], 1u);
+    else
+      atomicAdd(&a.counts[a.g0 + p], 1ull);
+  }
+  __syncthreads();
+  if (local)
+    for (int x = threadIdx.x; x < P; x += blockDim.x)
+      if (hist[x]) atomicAdd(&a.counts[a.g0 + x], static_cast<unsigned long long>(hist[x]));
+}
+
+// Workspace layout of a bulk call of P partitions (sub-calls of S positions).
+struct BulkLayout {
+  int64_t gt_cap, nch, off_mask, off_last, off_flag, off_scode, off_spos, off_src, bytes;
+};
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+BulkLayout bulk_layout(int64_t P, int64_t T) {
+  BulkLayout L{};
+  const int64_t S = T < kBulkSpan ? T : kBulkSpan;
+  int64_t cap = 1024;
+  while (cap < 2 * P * S) cap <<= 1;
+  L.gt_cap = cap;
+  L.nch = (S + kChunk - 1) / kChunk;
+  int64_t o = align256(cap * 8);
+  L.off_mask = o;
+  o += align256(cap * 8);
+  L.off_last = o;
+  o += align256(cap * 4);
+  L.off_flag = o;
+  o += align256(cap * 4);
+  L.off_scode = o;
+  o += align256(P * L.nch * kSlots * 4);
+  L.off_spos = o;
+  o += align256(P * L.nch * kSumPos * 4);
+  L.off_src = o;
+  o += align256(P * S * 4);
+  L.bytes = o;
+  return L;
+}
+
 }  // namespace
 }  // namespace lema
 
 using namespace lema;
 
-extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc,
-                                   const void* kc, int32_t code_bytes, const void* values,
-                                   void* out, int64_t n, int64_t T, int64_t g0, int64_t* counts,
-                                   int32_t* full, void* stream) {
+namespace {
+
+constexpr int64_t kBulkMinT = 2 * kChunk;  // longer calls with 32-bit codes take the bulk path
+
+bool bulk_applies(int64_t T, int32_t code_bytes) { return code_bytes == 4 && T > kBulkMinT; }
+
+int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
+  const int64_t P = a.n / a.T;
+  const BulkLayout L = bulk_layout(P, a.T);
+  LEMA_REQUIRE(workspace != nullptr && ws_bytes >= L.bytes && aligned(workspace, 256),
+               "workspace of %lld bytes (256-byte aligned) needed, got %lld", (long long)L.bytes,
+               (long long)ws_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  BulkWs w{};
+  w.gt_key = reinterpret_cast<uint64_t*>(ws);
+  w.gt_mask = reinterpret_cast<uint64_t*>(ws + L.off_mask);
+  w.gt_last = reinterpret_cast<int32_t*>(ws + L.off_last);
+  w.gt_flag = reinterpret_cast<int32_t*>(ws + L.off_flag);
+  w.sum_code = reinterpret_cast<uint32_t*>(ws + L.off_scode);
+  w.sum_pos = reinterpret_cast<int32_t*>(ws + L.off_spos);
+  w.src_in = reinterpret_cast<int32_t*>(ws + L.off_src);
+  w.gt_cap = L.gt_cap;
+  const int64_t slot_grid = (L.gt_cap * kGroup + 255) / 256;
+  const int64_t count_blocks = 1024;
+  const int64_t span = (L.gt_cap + count_blocks - 1) / count_blocks;
+  for (int64_t s0 = 0; s0 < a.T; s0 += kBulkSpan) {
+    a.s0 = s0;
+    a.len = static_cast<int32_t>(a.T - s0 < kBulkSpan ? a.T - s0 : kBulkSpan);
+    w.nch = (a.len + kChunk - 1) / kChunk;
+    bulk_clear_kernel<<<dim3(2048), dim3(256), 0, st>>>(w);
+    if (int rc = launch_status("bulk_clear_kernel")) return rc;
+    bulk_chunk_kernel<<<dim3(P * w.nch), dim3(kThreads), 0, st>>>(a, w);
+    if (int rc = launch_status("bulk_chunk_kernel")) return rc;
+    if (a.qc != nullptr) {
+      bulk_query_kernel<<<dim3((P * a.len * kGroup + 255) / 256), dim3(256), 0, st>>>(a, w);
+      if (int rc = launch_status("bulk_query_kernel")) return rc;
+    }
+    bulk_overwrite_kernel<<<dim3(slot_grid), dim3(256), 0, st>>>(a, w);
+    if (int rc = launch_status("bulk_overwrite_kernel")) return rc;
+    bulk_claim_kernel<<<dim3(slot_grid), dim3(256), 0, st>>>(a, w);
+    if (int rc = launch_status("bulk_claim_kernel")) return rc;
+    bulk_count_kernel<<<dim3(count_blocks), dim3(256), 0, st>>>(a, w, span);
+    if (int rc = launch_status("bulk_count_kernel")) return rc;
+  }
+  return LEMA_OK;
+}
+
+int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, const void* kc,
+                   int32_t code_bytes, const void* values, void* out, int64_t n, int64_t T,
+                   int64_t g0, int64_t* counts, int32_t* full, void* workspace, int64_t ws_bytes,
+                   void* stream) {
   clear_error();
   LEMA_REQUIRE(cap >= 1, "capacity must be positive, got %lld", (long long)cap);
   LEMA_REQUIRE(vbytes > 0 && vbytes % 8 == 0,
@@ -470,6 +815,11 @@ extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, con
     return launch_status("store_step_kernel");
   }
   LEMA_REQUIRE(P < (int64_t(1) << 31), "too many partitions (%lld)", (long long)P);
+  if (workspace != nullptr && bulk_applies(T, code_bytes)) {
+    LEMA_REQUIRE(P < (int64_t(1) << 31) - 1 && P * (T < kBulkSpan ? T : kBulkSpan) < (int64_t(1) << 31),
+                 "too many items per sub-call (%lld partitions)", (long long)P);
+    return run_bulk(a, workspace, ws_bytes, st);
+  }
   for (int64_t s0 = 0; s0 < T; s0 += kChunk) {
     a.s0 = s0;
     a.len = static_cast<int32_t>(T - s0 < kChunk ? T - s0 : kChunk);
@@ -480,4 +830,28 @@ extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, con
     if (int rc = launch_status("store_chunk_kernel")) return rc;
   }
   return LEMA_OK;
+}
+
+}  // namespace
+
+extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc,
+                                   const void* kc, int32_t code_bytes, const void* values,
+                                   void* out, int64_t n, int64_t T, int64_t g0, int64_t* counts,
+                                   int32_t* full, void* stream) {
+  return store_exchange(table, cap, vbytes, qc, kc, code_bytes, values, out, n, T, g0, counts,
+                        full, nullptr, 0, stream);
+}
+
+extern "C" int64_t lema_store_workspace_bytes(int64_t n, int64_t T, int32_t code_bytes) {
+  if (T <= 0 || n <= 0 || n % T != 0 || !bulk_applies(T, code_bytes)) return 0;
+  return bulk_layout(n / T, T).bytes;
+}
+
+extern "C" int lema_store_exchange_ws(void* table, int64_t cap, int64_t vbytes, const void* qc,
+                                      const void* kc, int32_t code_bytes, const void* values,
+                                      void* out, int64_t n, int64_t T, int64_t g0, int64_t* counts,
+                                      int32_t* full, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+  return store_exchange(table, cap, vbytes, qc, kc, code_bytes, values, out, n, T, g0, counts,
+                        full, workspace, workspace_bytes, stream);
 }

@@ -197,3 +197,85 @@ def test_decode_steps_in_a_graph_equal_eager(dev):
     assert torch.equal(graphed.view(torch.int16), eager.view(torch.int16))
     assert torch.equal(stores[1].counts, stores[0].counts)
     assert (eager[:, ::4] != 0).any(-1).float().mean() > 0.9
+
+
+# ------------------------------------------------------------------ the bulk path
+# Calls with int32 codes and T > 2048 run as sub-calls of up to 65536 positions with in-chunk
+# resolution, per-chunk key summaries and a scratch table of the sub-call's (partition, code)
+# pairs: the results must be the dict's in every case the chunked path covers.
+
+def test_bulk_one_shot_and_continued(dev):
+    """Two long calls in a row (5 chunks, the last partial): in-chunk, cross-chunk and
+    cross-call matches all occur."""
+    run_dict_case(dev, seed=11, P=5, T=9000, chunk=4500, n_codes=300, capacity=40_000,
+                  code_dtype=torch.int32)
+
+
+def test_bulk_crosses_a_sub_call(dev):
+    """T = 70,000: a sub-call of 65,536 positions and one of 4,464, in order; codes repeat
+    across the boundary."""
+    run_dict_case(dev, seed=12, P=2, T=70_000, chunk=70_000, n_codes=20_000,
+                  capacity=100_000, code_dtype=torch.int32)
+
+
+def test_bulk_hot_codes_in_every_chunk(dev):
+    """Eight codes over 30 chunks: every code's chunk mask is nearly full and queries whose
+    chunk lacks an earlier key take the latest chunk below theirs."""
+    run_dict_case(dev, seed=13, P=3, T=30_000, chunk=30_000, n_codes=8, capacity=1_000,
+                  code_dtype=torch.int32)
+
+
+def test_bulk_sentinel_and_zero_codes(dev):
+    """0xFFFFFFFF (int32 -1) is a code like any other, and so is 0."""
+    rng = np.random.default_rng(14)
+    P, T = 4, 6000
+    qc = rng.integers(0, 5, size=P * T).astype(np.int64) - 1        # -1 .. 3
+    kc = rng.integers(0, 5, size=P * T).astype(np.int64) - 1
+    far = rng.random(P * T) < 0.5                                    # queries that miss
+    qc[far] = rng.integers(10, 1 << 30, size=int(far.sum()))
+    vals = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=4096, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+    store.exchange(torch.from_numpy(qc).to(dev).to(torch.int32),
+                   torch.from_numpy(kc).to(dev).to(torch.int32),
+                   torch.from_numpy(vals.view(np.int16)).to(dev), out, T, 0)
+    # the dict sees the 32-bit patterns the store sees
+    want = ref.exchange(qc & 0xFFFFFFFF, kc & 0xFFFFFFFF, vals.view(np.uint8).reshape(-1, 2 * D_V),
+                        T, 0)
+    assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want)
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    assert set(store.dump()[1].cpu().numpy().tolist()) == {0xFFFFFFFF, 0, 1, 2, 3}
+
+
+def test_bulk_equals_chunked_path_and_insert_only(dev):
+    """The same long exchange through the bulk path (int32 codes) and the chunked path (int64
+    codes of the same values) leaves the same entries and returns the same values; an
+    insert-only long call then serves later queries."""
+    rng = np.random.default_rng(15)
+    P, T, cap = 6, 8192, 60_000
+    qc = rng.integers(0, 3000, size=P * T)
+    kc = rng.integers(0, 3000, size=P * T)
+    v = torch.from_numpy(rng.integers(-30000, 30000, size=(P * T, D_V), dtype=np.int16)).to(dev)
+    dumps, outs = [], []
+    for dt in (torch.int32, torch.int64):
+        st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+        out = torch.empty_like(v)
+        st.exchange(torch.from_numpy(qc).to(dev).to(dt), torch.from_numpy(kc).to(dev).to(dt),
+                    v, out, T, 0)
+        g, c, val = st.dump()
+        dumps.append({(int(a), int(b)): bytes(x) for a, b, x in
+                      zip(g.cpu().numpy(), c.cpu().numpy(), val.cpu().numpy())})
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]) and dumps[0] == dumps[1]
+    st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    st.exchange(None, torch.from_numpy(kc).to(dev).to(torch.int32), v, None, T, 0)
+    q = torch.from_numpy(kc.reshape(P, T)[:, ::2].copy()).to(dev).to(torch.int32).reshape(-1)
+    got = torch.empty((q.numel(), D_V), dtype=torch.int16, device=dev)
+    st.exchange(q, torch.full_like(q, -7), torch.zeros_like(got), got, T // 2, 0)
+    ref = oracle.DictStore(P, 2 * D_V)
+    vv = v.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V)
+    ref.exchange(np.full(P * T, -123), kc, vv, T, 0)
+    want = ref.exchange(q.cpu().numpy().astype(np.int64), np.full(q.numel(), (1 << 32) - 7),
+                        np.zeros((q.numel(), 2 * D_V), np.uint8), T // 2, 0)
+    assert np.array_equal(got.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want)
