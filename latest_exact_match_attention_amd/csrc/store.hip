@@ -426,18 +426,26 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
 //   queries  a query without an in-chunk answer takes the highest chunk below its own in its
 //            code's mask and that chunk's summary gives the key; with no such chunk it looks
 //            the store up (the table still holds exactly the keys before the sub-call);
-//   overwrite  every (partition, code) of the sub-call writes the value of its latest key over
-//            its existing store entry, or is marked;
-//   claim    marked codes claim store slots; a last pass counts the claims per partition.
-// The kernel boundaries order lookups before overwrites before claims, as the store needs.
+//   insert   every (partition, code) of the sub-call writes the value of its latest key over
+//            its existing store entry or claims a slot (code 0 in a kernel of its own, see
+//            bulk_insert_kernel); a last pass counts the claims per partition.
+// The kernel boundary orders every lookup of the sub-call before its inserts.
 constexpr int kBulkSpan = 64 * kChunk;  // positions per sub-call: chunk masks fit 64 bits
 constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots, the sentinel's
 
+// One (partition, code) of a sub-call: 32 bytes, so the claim and both updates of a chunk's
+// entry touch a single cache line.
+struct GroupSlot {
+  uint64_t key;    // (partition + 1) << 32 | code, 0 = free
+  uint64_t mask;   // bit c: chunk c of the sub-call holds keys with this code
+  int32_t last;    // latest key position of the code in the sub-call
+  int32_t flag;    // 2: claimed a store slot in this sub-call
+  uint64_t pad;
+};
+
 struct BulkWs {
-  uint64_t* gt_key;    // (partition + 1) << 32 | code, 0 = free
-  uint64_t* gt_mask;   // bit c: chunk c of the sub-call holds keys with this code
-  int32_t* gt_last;    // latest key position of the code in the sub-call
-  int32_t* gt_flag;    // 1: needs a store slot, 2: claimed one
+  GroupSlot* gt;
+  int64_t* zero_slot;  // per partition: group slot of code 0, or -1
   uint32_t* sum_code;  // per (partition, chunk): the kSlots key-code slots
   int32_t* sum_pos;    // per (partition, chunk): kSumPos latest positions
   int32_t* src_in;     // per query of the sub-call: in-chunk answer (sub-call position) or -1
@@ -453,11 +461,11 @@ __device__ __forceinline__ int64_t gt_home(uint64_t key, int64_t cap) {
 __device__ __forceinline__ int64_t gt_claim(const BulkWs& w, uint64_t key) {
   int64_t sl = gt_home(key, w.gt_cap);
   for (int64_t left = w.gt_cap; left > 0; --left) {
-    const uint64_t k = w.gt_key[sl];
+    const uint64_t k = w.gt[sl].key;
     if (k == key) return sl;
     if (k == 0) {
       const unsigned long long old =
-          atomicCAS(reinterpret_cast<unsigned long long*>(&w.gt_key[sl]), 0ull,
+          atomicCAS(reinterpret_cast<unsigned long long*>(&w.gt[sl].key), 0ull,
                     static_cast<unsigned long long>(key));
       if (old == 0 || old == key) return sl;
     }
@@ -470,7 +478,7 @@ __device__ __forceinline__ int64_t gt_claim(const BulkWs& w, uint64_t key) {
 __device__ __forceinline__ int64_t gt_find_group(const BulkWs& w, uint64_t key, int gl, int gbase) {
   int64_t base = gt_home(key, w.gt_cap);
   for (int64_t left = w.gt_cap; left > 0; left -= kGroup) {
-    const uint64_t k = w.gt_key[(base + gl) & (w.gt_cap - 1)];
+    const uint64_t k = w.gt[(base + gl) & (w.gt_cap - 1)].key;
     const Window win = window_bits<kGroup>(k == key, k == 0, gbase);
     const int fm = win.match ? first_bit(win.match) : kGroup;
     const int fe = win.empty ? first_bit(win.empty) : kGroup;
@@ -499,14 +507,12 @@ __device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int
   return -1;
 }
 
-__global__ __launch_bounds__(256) void bulk_clear_kernel(BulkWs w) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < w.gt_cap;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    w.gt_key[i] = 0;
-    w.gt_mask[i] = 0;
-    w.gt_last[i] = -1;
-    w.gt_flag[i] = 0;
-  }
+__global__ __launch_bounds__(256) void bulk_clear_kernel(BulkWs w, int64_t P) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = i0; i < w.gt_cap; i += stride)
+    w.gt[i] = GroupSlot{0ull, 0ull, -1, 0, 0ull};
+  for (int64_t i = i0; i < P; i += stride) w.zero_slot[i] = -1;
 }
 
 __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkWs w) {
@@ -573,8 +579,9 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
       atomicOr(a.full, 2);
       continue;
     }
-    atomicOr(reinterpret_cast<unsigned long long*>(&w.gt_mask[g]), 1ull << c);
-    atomicMax(&w.gt_last[g], c * kChunk + lp);
+    atomicOr(reinterpret_cast<unsigned long long*>(&w.gt[g].mask), 1ull << c);
+    atomicMax(&w.gt[g].last, c * kChunk + lp);
+    if (code == 0) w.zero_slot[p] = g;
   }
 }
 
@@ -593,7 +600,7 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
     const uint32_t code = static_cast<const uint32_t*>(a.qc)[base + o];
     const int c = o / kChunk;
     const int64_t g = gt_find_group(w, (static_cast<uint64_t>(p + 1) << 32) | code, gl, gbase);
-    const uint64_t m = g >= 0 ? (w.gt_mask[g] & ((1ull << c) - 1)) : 0;
+    const uint64_t m = g >= 0 ? (w.gt[g].mask & ((1ull << c) - 1)) : 0;
     if (m) {
       const int c2 = 63 - __clzll(m);
       const int64_t sum = p * w.nch + c2;
@@ -613,45 +620,46 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
   group_copy<kGroup>(a, dst, a.values + (base + j) * a.vbytes, gl);
 }
 
-__global__ __launch_bounds__(256) void bulk_overwrite_kernel(StoreArgs a, BulkWs w) {
+// Every (partition, code) of the sub-call, once: overwrite its store entry with the value of
+// its latest key, or claim a slot. The lookups of this sub-call are over (previous kernel), and
+// no other item looks for the same key, so the only thing a concurrent claim can be mistaken
+// for is code 0 (a claimed slot whose code is not written yet reads as 0): code-0 keys wait
+// for bulk_zero_kernel.
+__device__ __forceinline__ void bulk_insert_group(const StoreArgs& a, const BulkWs& w, int64_t g,
+                                                  int gl, int gbase) {
+  const uint64_t key = w.gt[g].key;
+  const int64_t p = static_cast<int64_t>(key >> 32) - 1;
+  const uint64_t code = key & 0xFFFFFFFFull;
+  const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
+  const int64_t h = home_slot(code, tag - 2, a.cap);
+  const uint8_t* v = a.values + (p * a.T + a.s0 + w.gt[g].last) * a.vbytes;
+  const int r = group_insert<kGroup>(a, code, tag, v, h, a.cap,
+                                     read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), false,
+                                     gl, gbase);
+  if (gl == 0) {
+    if (r > 0) w.gt[g].flag = 2;
+    if (r < 0) atomicOr(a.full, 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t g = gid / kGroup;
   const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
   if (g >= w.gt_cap) return;
-  const uint64_t key = w.gt_key[g];
-  if (key == 0) return;
-  const int64_t p = static_cast<int64_t>(key >> 32) - 1;
-  const uint64_t code = key & 0xFFFFFFFFull;
-  const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-  const int64_t h = home_slot(code, tag - 2, a.cap);
-  const int64_t sl = group_lookup<kGroup>(
-      a, code, tag, h, a.cap, read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), gl, gbase);
-  if (sl >= 0) {
-    const uint8_t* v = a.values + (p * a.T + a.s0 + w.gt_last[g]) * a.vbytes;
-    group_copy<kGroup>(a, a.table + sl * a.stride + 16, v, gl);
-  } else if (gl == 0) {
-    w.gt_flag[g] = 1;
-  }
+  const uint64_t key = w.gt[g].key;
+  if (key == 0 || (key & 0xFFFFFFFFull) == 0) return;
+  bulk_insert_group(a, w, g, gl, gbase);
 }
 
-__global__ __launch_bounds__(256) void bulk_claim_kernel(StoreArgs a, BulkWs w) {
+__global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, int64_t P) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t g = gid / kGroup;
+  const int64_t p = gid / kGroup;
   const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
-  if (g >= w.gt_cap || w.gt_flag[g] != 1) return;
-  const uint64_t key = w.gt_key[g];
-  const int64_t p = static_cast<int64_t>(key >> 32) - 1;
-  const uint64_t code = key & 0xFFFFFFFFull;
-  const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-  const int64_t h = home_slot(code, tag - 2, a.cap);
-  const uint8_t* v = a.values + (p * a.T + a.s0 + w.gt_last[g]) * a.vbytes;
-  const int r = group_insert<kGroup>(a, code, tag, v, h, a.cap,
-                                     read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), true,
-                                     gl, gbase);
-  if (gl == 0) {
-    if (r > 0) w.gt_flag[g] = 2;
-    if (r < 0) atomicOr(a.full, 1);
-  }
+  if (p >= P) return;
+  const int64_t g = w.zero_slot[p];
+  if (g < 0) return;
+  bulk_insert_group(a, w, g, gl, gbase);
 }
 
 // Claims per partition: a contiguous range of the group table per workgroup, counted in LDS
@@ -667,8 +675,8 @@ __global__ __launch_bounds__(256) void bulk_count_kernel(StoreArgs a, BulkWs w, 
   const int64_t g0 = static_cast<int64_t>(blockIdx.x) * span;
   const int64_t g1 = g0 + span < w.gt_cap ? g0 + span : w.gt_cap;
   for (int64_t g = g0 + threadIdx.x; g < g1; g += blockDim.x) {
-    if (w.gt_flag[g] != 2) continue;
-    const int64_t p = static_cast<int64_t>(w.gt_key[g] >> 32) - 1;
+    if (w.gt[g].flag != 2) continue;
+    const int64_t p = static_cast<int64_t>(w.gt[g].key >> 32) - 1;
     if (local)
       atomicAdd(&hist[p], 1u);
     else
@@ -682,7 +690,7 @@ __global__ __launch_bounds__(256) void bulk_count_kernel(StoreArgs a, BulkWs w, 
 
 // Workspace layout of a bulk call of P partitions (sub-calls of S positions).
 struct BulkLayout {
-  int64_t gt_cap, nch, off_mask, off_last, off_flag, off_scode, off_spos, off_src, bytes;
+  int64_t gt_cap, nch, off_zero, off_scode, off_spos, off_src, bytes;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -694,13 +702,9 @@ BulkLayout bulk_layout(int64_t P, int64_t T) {
   while (cap < 2 * P * S) cap <<= 1;
   L.gt_cap = cap;
   L.nch = (S + kChunk - 1) / kChunk;
-  int64_t o = align256(cap * 8);
-  L.off_mask = o;
-  o += align256(cap * 8);
-  L.off_last = o;
-  o += align256(cap * 4);
-  L.off_flag = o;
-  o += align256(cap * 4);
+  int64_t o = align256(cap * static_cast<int64_t>(sizeof(GroupSlot)));
+  L.off_zero = o;
+  o += align256(P * 8);
   L.off_scode = o;
   o += align256(P * L.nch * kSlots * 4);
   L.off_spos = o;
@@ -730,10 +734,8 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
                (long long)ws_bytes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   BulkWs w{};
-  w.gt_key = reinterpret_cast<uint64_t*>(ws);
-  w.gt_mask = reinterpret_cast<uint64_t*>(ws + L.off_mask);
-  w.gt_last = reinterpret_cast<int32_t*>(ws + L.off_last);
-  w.gt_flag = reinterpret_cast<int32_t*>(ws + L.off_flag);
+  w.gt = reinterpret_cast<GroupSlot*>(ws);
+  w.zero_slot = reinterpret_cast<int64_t*>(ws + L.off_zero);
   w.sum_code = reinterpret_cast<uint32_t*>(ws + L.off_scode);
   w.sum_pos = reinterpret_cast<int32_t*>(ws + L.off_spos);
   w.src_in = reinterpret_cast<int32_t*>(ws + L.off_src);
@@ -745,7 +747,7 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
     a.s0 = s0;
     a.len = static_cast<int32_t>(a.T - s0 < kBulkSpan ? a.T - s0 : kBulkSpan);
     w.nch = (a.len + kChunk - 1) / kChunk;
-    bulk_clear_kernel<<<dim3(2048), dim3(256), 0, st>>>(w);
+    bulk_clear_kernel<<<dim3(2048), dim3(256), 0, st>>>(w, P);
     if (int rc = launch_status("bulk_clear_kernel")) return rc;
     bulk_chunk_kernel<<<dim3(P * w.nch), dim3(kThreads), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_chunk_kernel")) return rc;
@@ -753,10 +755,10 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
       bulk_query_kernel<<<dim3((P * a.len * kGroup + 255) / 256), dim3(256), 0, st>>>(a, w);
       if (int rc = launch_status("bulk_query_kernel")) return rc;
     }
-    bulk_overwrite_kernel<<<dim3(slot_grid), dim3(256), 0, st>>>(a, w);
-    if (int rc = launch_status("bulk_overwrite_kernel")) return rc;
-    bulk_claim_kernel<<<dim3(slot_grid), dim3(256), 0, st>>>(a, w);
-    if (int rc = launch_status("bulk_claim_kernel")) return rc;
+    bulk_insert_kernel<<<dim3(slot_grid), dim3(256), 0, st>>>(a, w);
+    if (int rc = launch_status("bulk_insert_kernel")) return rc;
+    bulk_zero_kernel<<<dim3((P * kGroup + 255) / 256), dim3(256), 0, st>>>(a, w, P);
+    if (int rc = launch_status("bulk_zero_kernel")) return rc;
     bulk_count_kernel<<<dim3(count_blocks), dim3(256), 0, st>>>(a, w, span);
     if (int rc = launch_status("bulk_count_kernel")) return rc;
   }
