@@ -23,6 +23,10 @@
 // of each source row and the (non-temporal) writes of y are coalesced.
 #include "resolve_core.h"
 
+#ifndef LEMA_GATHER_INFLIGHT
+#define LEMA_GATHER_INFLIGHT 12  // value pieces in flight per thread (pieces a power of two)
+#endif
+
 namespace lema {
 namespace {
 
@@ -49,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
     __syncthreads();
     const int32_t c0 = chunk * kChunk;
     const int n_here = static_cast<int>(a.T - c0 < kChunk ? a.T - c0 : kChunk);
-    gather_rows<VEC, 8, 12>(a.g, row, c0, n_here, t, kThreads,
+    gather_rows<VEC, 8, LEMA_GATHER_INFLIGHT>(a.g, row, c0, n_here, t, kThreads,
                             [&](uint32_t r) -> int64_t { return srcs[r]; });
   }
 }

@@ -38,10 +38,18 @@ __device__ __forceinline__ int bucket_of(uint32_t x) {
 constexpr int kThreads = 256;
 constexpr int kPer = 4;
 constexpr int kChunk = kThreads * kPer;
-constexpr int kSlots = 2 * kChunk;  // query-code table: at most kChunk codes, load <= 1/2
+#ifndef LEMA_RESOLVE_SLOTS
+#define LEMA_RESOLVE_SLOTS 2048
+#endif
+#ifndef LEMA_RESOLVE_MAP_SLOTS
+#define LEMA_RESOLVE_MAP_SLOTS 1536
+#endif
+constexpr int kSlots = LEMA_RESOLVE_SLOTS;  // query-code table: at most kChunk codes
 constexpr int kBuckets = kSlots / 4;
-constexpr int kMapSlots = 3 * kChunk / 2;  // (code slot, word) -> lane mask: at most kChunk
-constexpr int kMapBuckets = kMapSlots / 4;  // keys, load <= 2/3
+constexpr int kMapSlots = LEMA_RESOLVE_MAP_SLOTS;  // (code slot, word) -> lane mask: at most
+constexpr int kMapBuckets = kMapSlots / 4;          // kChunk keys
+static_assert(kSlots > kChunk && kSlots % 4 == 0 && kMapSlots > kChunk && kMapSlots % 4 == 0,
+              "tables must keep free slots");
 constexpr uint32_t kMapEmpty = 0xFFFFFFFFu;
 static_assert(kChunk / 64 <= 16, "word summary is a 16-bit mask");
 

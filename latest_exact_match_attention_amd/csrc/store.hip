@@ -431,6 +431,7 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
 //            bulk_insert_kernel); a last pass counts the claims per partition.
 // The kernel boundary orders every lookup of the sub-call before its inserts.
 constexpr int kBulkSpan = 64 * kChunk;  // positions per sub-call: chunk masks fit 64 bits
+static_assert((kSlots & (kSlots - 1)) == 0, "chunk summaries are probed with a slot mask");
 constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots, the sentinel's
 
 // One (partition, code) of a sub-call: 32 bytes, so the claim and both updates of a chunk's
