@@ -414,6 +414,13 @@ def bench_lm(a):
         src = torch.empty((B, cfg.num_heads, T), dtype=torch.int32, device=dev)
         launch_hard(qc, kc, v, yv, src)
         hits = float((src >= 0).float().mean())
+        # the sign-pack alone on the layer's query pre-activations (transposed view, bf16)
+        e0.record(stream)
+        for _ in range(n_l):
+            pack_codes(zq, torch.int32)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_p = e0.elapsed_time(e1) / n_l
     ntok = B * T
     flops = lm_flops_per_token(cfg) * ntok
     tflops = flops / (ms * 1e-3) / 1e12
@@ -444,6 +451,10 @@ def bench_lm(a):
         "lema_kernel": {"kernel": "resolve_kernel (fused resolve + gather), one layer",
                         "us": ms_l * 1e3, "queries": nq, "bytes_per_query": bpq,
                         "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS},
+        "pack_kernel": {"kernel": "pack_dense_kernel, one layer's query codes",
+                        "us": ms_p * 1e3, "rows": nq, "bytes_per_row": 2 * cfg.d_qk + 4,
+                        "achieved_gbs": (2 * cfg.d_qk + 4) * nq / (ms_p * 1e-3) / 1e9,
+                        "frac": (2 * cfg.d_qk + 4) * nq / (ms_p * 1e-3) / 1e9 / HBM_PEAK_GBS},
         "cpu_baseline": cpu,
     }
 

@@ -3,11 +3,11 @@
 // Bit j of the code of a row is (z_j >= 0) as a float compare: -0.0 -> 1, NaN -> 0, LSB = dim 0.
 //
 // Dense path (the rows form one packed array in some order of (b, h, t), as for both a
-// contiguous [B, H, T, D] tensor and the transposed [B, T, H, D] projection view): a wavefront
-// takes 64 consecutive rows in MEMORY order, i.e. 64*D consecutive elements. In D steps each
-// lane loads one element (coalesced) and a wavefront ballot turns the 64 sign tests into one
-// 64-bit word of the rows' concatenated bit string; lane l then cuts its row's D bits out of
-// those words (staged in LDS) and writes the code to its (b, h, t) slot.
+// contiguous [B, H, T, D] tensor and the transposed [B, T, H, D] projection view, 16-byte
+// aligned): a wavefront takes 64 consecutive rows in MEMORY order, i.e. 64*D consecutive
+// elements; each lane turns 8 consecutive elements (one 16-byte load) into one byte of the
+// rows' concatenated bit string in LDS, and lane l then cuts its row's D bits out of it and
+// writes the code to its (b, h, t) slot.
 // Generic path (any strides, last dim contiguous): one thread per row.
 #include "lema_internal.h"
 
@@ -40,6 +40,55 @@ struct DenseArgs {
 
 constexpr int kPackThreads = 256;
 
+// One lane's 8 consecutive elements: 16 bytes (32 for fp32), loaded before any is tested.
+template <int DTYPE>
+struct Raw8 {
+  u32x4 v[DTYPE == LEMA_F32 ? 2 : 1];
+};
+
+template <int DTYPE>
+__device__ __forceinline__ Raw8<DTYPE> load8(const void* z, int64_t e) {
+  Raw8<DTYPE> r;
+  if constexpr (DTYPE == LEMA_F32) {
+    r.v[0] = *reinterpret_cast<const u32x4*>(static_cast<const float*>(z) + e);
+    r.v[1] = *reinterpret_cast<const u32x4*>(static_cast<const float*>(z) + e + 4);
+  } else {
+    r.v[0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(z) + e);
+  }
+  return r;
+}
+
+// Sign bits of the 8 elements, bit k = element k.
+template <int DTYPE>
+__device__ __forceinline__ uint32_t sign_byte(const Raw8<DTYPE>& r) {
+  uint32_t m = 0;
+  if constexpr (DTYPE == LEMA_F32) {
+    const uint32_t w[8] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w,
+                           r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m |= (__uint_as_float(w[k]) >= 0.0f ? 1u : 0u) << k;
+  } else {
+    const uint32_t w[4] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t h = (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      bool b;
+      if constexpr (DTYPE == LEMA_BF16) {
+        b = __uint_as_float(h << 16) >= 0.0f;
+      } else {  // IEEE half on its bits: NaN -> false, -0 -> true
+        b = !((h & 0x7C00u) == 0x7C00u && (h & 0x03FFu) != 0) &&
+            ((h & 0x8000u) == 0 || (h & 0x7FFFu) == 0);
+      }
+      m |= (b ? 1u : 0u) << k;
+    }
+  }
+  return m;
+}
+
+// Dense path: a wavefront owns 64 consecutive rows in memory order, i.e. 64*D consecutive
+// elements. Each lane reads 16 (32 for fp32) bytes per step -- 8 elements, their 8 sign bits
+// one byte of the rows' concatenated bit string, staged in LDS -- so the wavefront covers
+// the string in ceil(D / 8) coalesced steps; lane l then cuts row l's D bits out of it.
 template <int DTYPE, typename CodeT>
 __global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
   __shared__ uint64_t words[kPackThreads / 64][64 + 1];
@@ -47,11 +96,31 @@ __global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
   const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * (kPackThreads / 64) + w) * 64;
   if (m0 >= a.R) return;
   const int64_t e0 = m0 * a.D, eend = a.R * a.D;
-  for (int it = 0; it < a.D; ++it) {
-    const int64_t e = e0 + static_cast<int64_t>(it) * 64 + lane;
-    const bool bit = e < eend && nonneg<DTYPE>(a.z, e);
-    const uint64_t word = __ballot(bit);
-    if (lane == 0) words[w][it] = word;
+  uint8_t* bytes = reinterpret_cast<uint8_t*>(words[w]);
+  const int steps = (a.D + 7) / 8;  // 8 * D bytes of bit string, 64 bytes per step
+  const bool whole = e0 + 64 * static_cast<int64_t>(a.D) <= eend;  // no array end inside
+  if (whole) {
+    Raw8<DTYPE> raw[8];  // every load of the lane in flight before the first test
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int b = it * 64 + lane;
+      if (it < steps && b < 8 * a.D) raw[it] = load8<DTYPE>(a.z, e0 + static_cast<int64_t>(b) * 8);
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int b = it * 64 + lane;
+      if (it < steps && b < 8 * a.D) bytes[b] = static_cast<uint8_t>(sign_byte<DTYPE>(raw[it]));
+    }
+  } else {  // the array's last rows: element by element
+    for (int it = 0; it < steps; ++it) {
+      const int b = it * 64 + lane;
+      if (b >= 8 * a.D) continue;
+      const int64_t e = e0 + static_cast<int64_t>(b) * 8;
+      uint32_t m = 0;
+      for (int k = 0; k < 8; ++k)
+        if (e + k < eend && nonneg<DTYPE>(a.z, e + k)) m |= 1u << k;
+      bytes[b] = static_cast<uint8_t>(m);
+    }
   }
   if (lane == 0) words[w][a.D] = 0;
   __builtin_amdgcn_wave_barrier();
@@ -154,7 +223,7 @@ extern "C" int lema_pack_codes(const void* z, int32_t dtype, int64_t B, int64_t 
     dense = dense && kept[i].s == need;
     need *= kept[i].e;
   }
-  if (dense) {
+  if (dense && aligned(z, 16)) {
     Dim full[3] = {{1, 0, 0}, {1, 0, 0}, {1, 0, 0}};
     for (int i = 0; i < nk; ++i) full[3 - nk + i] = kept[i];
     DenseArgs a{z, codes, R, full[1].e, full[2].e, full[0].os, full[1].os, full[2].os, D};
