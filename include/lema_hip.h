@@ -109,6 +109,25 @@ int lema_store_exchange_ws(void* table, int64_t cap, int64_t vbytes, const void*
                            int64_t n, int64_t T, int64_t g0, int64_t* counts, int32_t* full,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- fused model segments (bf16), what the reference compiles with torch.compile ---- */
+
+/* out = silu(gate) * up over n bf16 elements (n % 8 == 0, 16-byte aligned), the silu rounded
+ * to bf16 first as in SwiGLU.forward, code/lema/model.py:85-94. */
+int lema_swiglu_bf16(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/* Pre-norm of a block: x_out = x + d (d may be NULL: then x_out is unused), h_out =
+ * x_out / sqrt(mean(x_out^2) + eps) * w, rows of D bf16 (D % 8 == 0, D <= 4096, 16-byte
+ * aligned). Replaces the residual add and nn.RMSNorm of Block.forward,
+ * code/lema/model.py:212-255. */
+int lema_rmsnorm_bf16(const void* x, const void* d, const void* w, float eps, int64_t rows,
+                      int64_t D, void* x_out, void* h_out, void* stream);
+
+/* loss[r] = logsumexp(logits[r, :V]) - logits[r, target[r]] from bf16 logits (row stride ld,
+ * V and ld multiples of 8, targets in [0, V)), fp32. Replaces the per-chunk
+ * F.cross_entropy(logits.float()) of code/lema/train.py:131-152. */
+int lema_cross_entropy_bf16(const void* logits, int64_t rows, int64_t V, int64_t ld,
+                            const int64_t* target, float* loss, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

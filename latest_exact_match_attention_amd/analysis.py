@@ -15,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from .attention import latest_prev_match, pack_codes
+from .model import rms_norm
 
 __all__ = ["trace", "prefix_distinct", "census", "LemaState"]
 
@@ -97,8 +98,8 @@ class LemaState:
 
     @torch.no_grad()
     def prefill(self, x):
-        return self.model.norm_f(self._run(x)[:, -1:])
+        return rms_norm(self._run(x)[:, -1:].contiguous(), self.model.norm_f)[0]
 
     @torch.no_grad()
     def step(self, tok):
-        return self.model.norm_f(self._run(tok))
+        return rms_norm(self._run(tok), self.model.norm_f)[0]

@@ -1,0 +1,214 @@
+// Fused elementwise and normalisation kernels of the LEMA language model's forward in bf16
+// (code/lema/model.py:85-94, 212-255, code/lema/train.py:131-152). The reference compiles
+// these segments with torch.compile; here each is one hand-written pass over HBM:
+//   swiglu      out = silu(gate) * up, with the intermediate rounded to bf16 as the two torch
+//               ops round it (SwiGLU.forward);
+//   rmsnorm     x_out = x + d (optional residual, rounded to bf16), h = x_out * rsqrt(mean(
+//               x_out^2) + eps) * w (Block's pre-norms, the final norm);
+//   xent        per row, logsumexp(logits) - logits[target] from bf16 logits in fp32, one read
+//               of the row (online max and rescaled sum), instead of a fp32 copy plus a
+//               softmax pass.
+#include "lema_internal.h"
+
+namespace lema {
+namespace {
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Round to nearest even, NaN to the canonical quiet NaN (as torch's bfloat16 conversion).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  const uint32_t b = __float_as_uint(f);
+  if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu) != 0) return 0x7FC0u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
+  uint32_t out = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float g = bf16_to_f32((g2 >> (16 * k)) & 0xFFFFu);
+    const float u = bf16_to_f32((u2 >> (16 * k)) & 0xFFFFu);
+    const float s = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
+    out |= f32_to_bf16(s * u) << (16 * k);
+  }
+  return out;
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const u32x4* gate, const u32x4* up,
+                                                     u32x4* out, int64_t n8) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const u32x4 g = gate[i], u = up[i];
+    out[i] = u32x4{swiglu_pair(g.x, u.x), swiglu_pair(g.y, u.y), swiglu_pair(g.z, u.z),
+                   swiglu_pair(g.w, u.w)};
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// One wavefront per row of D bf16 (D % 8 == 0), 8 elements per lane per step.
+constexpr int kNormMaxSteps = 8;  // D <= 64 lanes * 8 * 8 = 4096
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* d,
+                                                      const uint16_t* w, float eps, int64_t rows,
+                                                      int D, uint16_t* x_out, uint16_t* h_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int steps = D / 512 + (D % 512 ? 1 : 0);
+  u32x4 xv[kNormMaxSteps];
+  float ss = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kNormMaxSteps; ++s) {
+    const int e = (s * 64 + lane) * 8;
+    if (s >= steps || e >= D) continue;
+    u32x4 v = *reinterpret_cast<const u32x4*>(x + row * D + e);
+    if (d != nullptr) {
+      const u32x4 dv = *reinterpret_cast<const u32x4*>(d + row * D + e);
+      uint32_t* pv = reinterpret_cast<uint32_t*>(&v);
+      const uint32_t* pd = reinterpret_cast<const uint32_t*>(&dv);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = f32_to_bf16(bf16_to_f32(pv[k] & 0xFFFFu) + bf16_to_f32(pd[k] & 0xFFFFu));
+        const uint32_t hi = f32_to_bf16(bf16_to_f32(pv[k] >> 16) + bf16_to_f32(pd[k] >> 16));
+        pv[k] = lo | (hi << 16);
+      }
+      *reinterpret_cast<u32x4*>(x_out + row * D + e) = v;
+    }
+    xv[s] = v;
+    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = bf16_to_f32(pv[k] & 0xFFFFu), b = bf16_to_f32(pv[k] >> 16);
+      ss += a * a + b * b;
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int s = 0; s < kNormMaxSteps; ++s) {
+    const int e = (s * 64 + lane) * 8;
+    if (s >= steps || e >= D) continue;
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + e);
+    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&xv[s]);
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(&wv);
+    u32x4 o;
+    uint32_t* po = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = f32_to_bf16(bf16_to_f32(pv[k] & 0xFFFFu) * rstd * bf16_to_f32(pw[k] & 0xFFFFu));
+      const uint32_t hi = f32_to_bf16(bf16_to_f32(pv[k] >> 16) * rstd * bf16_to_f32(pw[k] >> 16));
+      po[k] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(h_out + row * D + e) = o;
+  }
+}
+
+// One workgroup (256 threads) per row of V bf16 logits (V % 8 == 0, rows 16-byte aligned):
+// each thread keeps a running max and a sum rescaled to it, then the workgroup combines them.
+__global__ __launch_bounds__(256) void xent_kernel(const uint16_t* logits, int64_t V, int64_t ld,
+                                                   const int64_t* target, float* loss) {
+  __shared__ float smax[4], ssum[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* r = logits + row * ld;
+  float m = -INFINITY, s = 0.0f;
+  for (int64_t e = static_cast<int64_t>(threadIdx.x) * 8; e < V; e += 256 * 8) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(r + e);
+    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&v);
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = bf16_to_f32(pv[k] & 0xFFFFu);
+      x[2 * k + 1] = bf16_to_f32(pv[k] >> 16);
+    }
+    float bm = x[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) bm = fmaxf(bm, x[k]);
+    if (bm > m) {
+      s *= expf(m - bm);
+      m = bm;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += expf(x[k] - m);
+  }
+  // combine: wavefront, then the 4 wavefronts
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float om = __shfl_xor(m, o), os = __shfl_xor(s, o);
+    const float nm = fmaxf(m, om);
+    s = (m == -INFINITY ? 0.0f : s * expf(m - nm)) + (om == -INFINITY ? 0.0f : os * expf(om - nm));
+    m = nm;
+  }
+  const int wv = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    smax[wv] = m;
+    ssum[wv] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = smax[0];
+    for (int k = 1; k < 4; ++k) M = fmaxf(M, smax[k]);
+    float S = 0.0f;
+    for (int k = 0; k < 4; ++k) S += smax[k] == -INFINITY ? 0.0f : ssum[k] * expf(smax[k] - M);
+    const int64_t t = target[row];
+    const float xt = (t >= 0 && t < V) ? bf16_to_f32(r[t]) : NAN;
+    loss[row] = logf(S) + M - xt;
+  }
+}
+
+}  // namespace
+}  // namespace lema
+
+using namespace lema;
+
+extern "C" int lema_swiglu_bf16(const void* gate, const void* up, void* out, int64_t n,
+                                void* stream) {
+  clear_error();
+  LEMA_REQUIRE(n >= 0 && n % 8 == 0, "element count %lld must be a multiple of 8", (long long)n);
+  if (n == 0) return LEMA_OK;
+  LEMA_REQUIRE(gate && up && out && aligned(gate, 16) && aligned(up, 16) && aligned(out, 16),
+               "gate, up and out must be 16-byte aligned device pointers");
+  const int64_t n8 = n / 8;
+  int64_t grid = (n8 + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  swiglu_kernel<<<dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4*>(gate), static_cast<const u32x4*>(up), static_cast<u32x4*>(out), n8);
+  return launch_status("swiglu_kernel");
+}
+
+extern "C" int lema_rmsnorm_bf16(const void* x, const void* d, const void* w, float eps,
+                                 int64_t rows, int64_t D, void* x_out, void* h_out, void* stream) {
+  clear_error();
+  LEMA_REQUIRE(rows >= 0 && D > 0 && D % 8 == 0 && D <= 64 * 8 * kNormMaxSteps,
+               "row length %lld must be a multiple of 8 and at most %d", (long long)D,
+               64 * 8 * kNormMaxSteps);
+  if (rows == 0) return LEMA_OK;
+  LEMA_REQUIRE(x && w && h_out && (d == nullptr || x_out != nullptr), "null pointer");
+  LEMA_REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(h_out, 16) &&
+                   (d == nullptr || (aligned(d, 16) && aligned(x_out, 16))),
+               "pointers must be 16-byte aligned");
+  const int64_t grid = (rows + 3) / 4;
+  LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows");
+  rmsnorm_kernel<<<dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d),
+      static_cast<const uint16_t*>(w), eps, rows, static_cast<int>(D),
+      static_cast<uint16_t*>(x_out), static_cast<uint16_t*>(h_out));
+  return launch_status("rmsnorm_kernel");
+}
+
+extern "C" int lema_cross_entropy_bf16(const void* logits, int64_t rows, int64_t V, int64_t ld,
+                                       const int64_t* target, float* loss, void* stream) {
+  clear_error();
+  LEMA_REQUIRE(rows >= 0 && V > 0 && V % 8 == 0 && ld >= V && ld % 8 == 0,
+               "vocabulary %lld and row stride %lld must be multiples of 8", (long long)V,
+               (long long)ld);
+  if (rows == 0) return LEMA_OK;
+  LEMA_REQUIRE(logits && target && loss && aligned(logits, 16) && aligned(target, 8) &&
+                   aligned(loss, 4), "bad pointer");
+  LEMA_REQUIRE(rows < (int64_t(1) << 31), "too many rows");
+  xent_kernel<<<dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(logits), V, ld, target, loss);
+  return launch_status("xent_kernel");
+}

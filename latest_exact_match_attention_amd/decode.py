@@ -19,6 +19,7 @@ import contextlib
 import torch
 
 from .cache import HashStore, LemaCache
+from .model import rms_norm
 
 __all__ = ["LemaDecoder", "decoder", "worst_case_codes"]
 
@@ -81,7 +82,7 @@ class LemaDecoder:
             for i in range(L):
                 qc, kc, v = segs[i][0](x)
                 x = segs[i][1](x, views[i].exchange(qc, kc, v, check=False))
-            logits = model.lm_head(model.norm_f(x))
+            logits = model.lm_head(rms_norm(x, model.norm_f)[0])
             self.tok.copy_(choose(logits))
             return logits
 

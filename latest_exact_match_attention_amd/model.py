@@ -14,6 +14,10 @@ block norm1, q, k, v, o, norm2, gate, up, down, then norm_f, lm_head; Gaussian s
 outputs scaled by 1/sqrt(2 * depth): code/lema/model.py:258-281), so the same seed gives the
 same weights.
 
+In bf16 on the GPU the SwiGLU product, the attention residual add with the MLP's pre-norm, the
+final norm and the loss run as fused HIP kernels (the reference compiles these segments with
+torch.compile). The attention pre-norm, whose output decides the codes, stays torch's RMSNorm.
+
 Only the hard (exact) op is implemented: the training surrogate (stick-breaking relaxation,
 straight-through binarization) and the softmax / gated-deltanet baselines are not part of the
 exact-match path.
@@ -28,9 +32,59 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _lib
 from .attention import code_dtype_for, lema_hard, pack_codes
 
-__all__ = ["ModelConfig", "SwiGLU", "Attention", "Block", "Transformer", "lm_loss"]
+__all__ = ["ModelConfig", "SwiGLU", "Attention", "Block", "Transformer", "lm_loss", "rms_norm",
+           "swiglu", "cross_entropy_sum"]
+
+# ------------------------------------------------------------------ fused bf16 segments
+# On the GPU in bf16 the SwiGLU product, the residual add with the next pre-norm, and the loss
+# run as one HIP kernel each (liblema_hip.so); other dtypes and devices use the torch ops.
+
+def _fused(*ts: torch.Tensor) -> bool:
+    return all(t.is_cuda and t.dtype == torch.bfloat16 and t.is_contiguous() for t in ts)
+
+
+def rms_norm(x: torch.Tensor, norm: nn.RMSNorm, d: torch.Tensor | None = None):
+    """norm(x + d) and x + d (or norm(x), x when d is None), one pass in bf16."""
+    if d is not None and not (_fused(x, d) and _fused(norm.weight)):
+        x, d = x + d, None
+    if not (_fused(x) and _fused(norm.weight) and x.shape[-1] % 8 == 0
+            and x.shape[-1] <= 4096):
+        return norm(x), x
+    D = x.shape[-1]
+    h = torch.empty_like(x)
+    xo = torch.empty_like(x) if d is not None else x
+    eps = norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
+    _lib.check(_lib.lib().lema_rmsnorm_bf16(
+        x.data_ptr(), d.data_ptr() if d is not None else None, norm.weight.data_ptr(),
+        float(eps), x.numel() // D, D, xo.data_ptr() if d is not None else None, h.data_ptr(),
+        _lib.stream_of(x)))
+    return h, xo
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    if not (_fused(g, u) and g.numel() % 8 == 0):
+        return F.silu(g) * u
+    out = torch.empty_like(g)
+    _lib.check(_lib.lib().lema_swiglu_bf16(g.data_ptr(), u.data_ptr(), out.data_ptr(),
+                                           g.numel(), _lib.stream_of(g)))
+    return out
+
+
+def cross_entropy_sum(logits: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """Sum over rows of logsumexp(logits) - logits[y] (fp32)."""
+    V = logits.shape[-1]
+    if not (_fused(logits) and V % 8 == 0 and y.is_cuda):
+        return F.cross_entropy(logits.float(), y, reduction="sum")
+    rows = logits.numel() // V
+    loss = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    yy = y.reshape(-1).to(torch.int64).contiguous()
+    _lib.check(_lib.lib().lema_cross_entropy_bf16(
+        logits.data_ptr(), rows, V, V, yy.data_ptr(), loss.data_ptr(), _lib.stream_of(logits)))
+    return loss.sum()
+
 
 ATTN_KINDS = ("lema",)
 POS_KINDS = ("nope",)
@@ -97,7 +151,7 @@ class SwiGLU(nn.Module):
         self.down = nn.Linear(dim_ff, dim, bias=False)
 
     def forward(self, x):
-        return self.down(F.silu(self.gate(x)) * self.up(x))
+        return self.down(swiglu(self.gate(x), self.up(x)))
 
 
 class Attention(nn.Module):
@@ -155,16 +209,16 @@ class Block(nn.Module):
 
     def gpu_post(self, x, got):
         """Merge the retrieved values and finish the layer (code/lema/model.py:229-232)."""
-        x = x + self.attn.merge(got)
-        return x + self.mlp(self.norm2(x))
+        h, x = rms_norm(x, self.norm2, self.attn.merge(got))
+        return x + self.mlp(h)
 
     def forward(self, x, store=None):
         if store is not None:
             pre, post = self.seg or (self.gpu_pre, self.gpu_post)
             qc, kc, v = pre(x)
             return post(x, store.exchange(qc, kc, v))
-        x = x + self.attn(self.norm1(x))
-        return x + self.mlp(self.norm2(x))
+        h, x = rms_norm(x, self.norm2, self.attn(self.norm1(x)))
+        return x + self.mlp(h)
 
 
 class Transformer(nn.Module):
@@ -226,14 +280,14 @@ class Transformer(nn.Module):
             x = blk(x, store=(cache.layer(li) if cache is not None else None))
         if cache is not None:
             cache.t += idx.shape[-1]
-        return self.lm_head(self.norm_f(x)) if return_logits else None
+        return self.lm_head(rms_norm(x, self.norm_f)[0]) if return_logits else None
 
     def hidden(self, idx):
         """The final normalised hidden states (the input of lm_head), without a cache."""
         x = self.tok_emb(idx)
         for blk in self.blocks:
             x = blk(x)
-        return self.norm_f(x)
+        return rms_norm(x, self.norm_f)[0]
 
     def n_params(self, embedding: bool = True) -> int:
         n = sum(p.numel() for p in self.parameters())
@@ -252,7 +306,5 @@ def lm_loss(model: Transformer, x: torch.Tensor, y: torch.Tensor, chunk: int = 1
         # a contiguous 2-D block: the head is then one plain GEMM (a strided 3-D slice would
         # make matmul broadcast the transposed weight into a batched product instead)
         hc = h[:, a:a + chunk].reshape(-1, h.shape[-1]).contiguous()
-        logits = model.lm_head(hc)
-        total += F.cross_entropy(logits.float(), y[:, a:a + chunk].reshape(-1),
-                                 reduction="sum")
+        total += cross_entropy_sum(model.lm_head(hc), y[:, a:a + chunk].reshape(-1))
     return total / y.numel()

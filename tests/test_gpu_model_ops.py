@@ -1,0 +1,54 @@
+"""The fused bf16 model segments against the torch ops they replace (plain PyTorch
+references: F.silu(g) * u, nn.RMSNorm after a bf16 add, F.cross_entropy on fp32 logits)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from latest_exact_match_attention_amd.model import cross_entropy_sum, rms_norm, swiglu
+
+pytestmark = pytest.mark.gpu
+
+
+def ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in bf16 units in the last place (same-sign finite values)."""
+    ia, ib = a.view(torch.int16).int(), b.view(torch.int16).int()
+    return (ia - ib).abs()
+
+
+def test_swiglu_matches_silu_times_up(dev):
+    g = (torch.randn(4096, 6144, device=dev) * 3).to(torch.bfloat16)
+    u = torch.randn(4096, 6144, device=dev).to(torch.bfloat16)
+    g[0, :6] = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 88.0, -88.0])
+    got = swiglu(g, u)
+    want = F.silu(g) * u
+    fin = torch.isfinite(want)
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    d = ulps(got[fin], want[fin])
+    assert (d == 0).float().mean() > 0.999 and d.max() <= 1, (d.max(), (d == 0).float().mean())
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_rmsnorm_matches_torch(dev, residual):
+    D = 1536
+    norm = torch.nn.RMSNorm(D, eps=1e-5).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(D, device=dev))
+    x = torch.randn(3000, D, device=dev).to(torch.bfloat16)
+    d = torch.randn(3000, D, device=dev).to(torch.bfloat16) if residual else None
+    with torch.no_grad():
+        h, xo = rms_norm(x, norm, d)
+        xr = x + d if residual else x
+        assert torch.equal(xo, xr)                       # the bf16 add, exactly
+        want = norm(xr)
+    rel = ((h.float() - want.float()).abs() / want.float().abs().clamp_min(1e-2)).max()
+    assert rel <= 2 ** -7, rel                            # within one bf16 rounding
+    assert (h == want).float().mean() > 0.95
+
+
+def test_cross_entropy_from_bf16_logits(dev):
+    V = 50304
+    logits = (torch.randn(1000, V, device=dev) * 4).to(torch.bfloat16)
+    y = torch.randint(0, V, (1000,), device=dev)
+    got = cross_entropy_sum(logits, y)
+    want = F.cross_entropy(logits.float(), y, reduction="sum")
+    assert abs(got.item() - want.item()) <= 1e-5 * abs(want.item())
