@@ -279,3 +279,29 @@ def test_bulk_equals_chunked_path_and_insert_only(dev):
     want = ref.exchange(q.cpu().numpy().astype(np.int64), np.full(q.numel(), (1 << 32) - 7),
                         np.zeros((q.numel(), 2 * D_V), np.uint8), T // 2, 0)
     assert np.array_equal(got.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want)
+
+
+def test_bulk_many_partitions_equals_chunked_path(dev):
+    """4,200 partitions (more than the count kernel's LDS histogram holds) x T = 2,100: the
+    bulk path (int32 codes) and the chunked path (int64 codes) agree on outputs, entries and
+    per-partition counts."""
+    rng = np.random.default_rng(16)
+    P, T, cap = 4200, 2100, 9_000_000
+    qc = rng.integers(0, 700, size=P * T)
+    kc = rng.integers(0, 700, size=P * T)
+    v = torch.from_numpy(rng.integers(-30000, 30000, size=(P * T, D_V), dtype=np.int16)).to(dev)
+    outs, dumps, counts = [], [], []
+    for dt in (torch.int32, torch.int64):
+        st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+        out = torch.empty_like(v)
+        st.exchange(torch.from_numpy(qc).to(dev).to(dt), torch.from_numpy(kc).to(dev).to(dt),
+                    v, out, T, 0)
+        g, c, val = st.dump()
+        key = g * 1024 + c                                   # codes < 700, groups < 4200
+        order = torch.argsort(key)
+        dumps.append((key[order], val[order]))
+        outs.append(out)
+        counts.append(st.counts)
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(dumps[0][0], dumps[1][0]) and torch.equal(dumps[0][1], dumps[1][1])
+    assert torch.equal(counts[0], counts[1]) and int(counts[0].sum()) == dumps[0][0].numel()
