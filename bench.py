@@ -562,7 +562,7 @@ def bench_long(a):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got "
+        print(f"bench.py measures one GPU only (there is no multi-GPU path); got "
               f"--gpus {a.gpus}", file=sys.stderr)
         return 2
     run = {"decode": bench_decode, "lm_forward": bench_lm,

@@ -1,7 +1,7 @@
 """CPU oracle for the LEMA hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only `tests/`, `__graft_entry__.smoke()` and the CPU-baseline leg of `bench.py` import this
-package, and only as the checker or as the timed CPU counterpart. The product
+package, and only as the oracle of the parity checks or as the timed CPU counterpart. The product
 (`latest_exact_match_attention_amd`) never imports it and has no CPU fallback.
 
 Contents:

@@ -2,7 +2,7 @@
  *
  * Nothing in the product (the HIP library and the Python package above it) links, loads or
  * calls this file. Only the tests, the smoke check and the CPU-baseline leg of the benchmark
- * use it, and only as the checker / the timed CPU counterpart.
+ * use it, and only as the oracle of the parity checks / the timed CPU counterpart.
  *
  * Each function restates one piece of the reference's behaviour, cited as file:line of
  * moritzbroe/latest_exact_match_attention:

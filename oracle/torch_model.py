@@ -1,5 +1,5 @@
 """The LEMA language model's forward restated functionally in plain torch -- TEST
-INFRASTRUCTURE ONLY (the checker of the model path; the product never imports it).
+INFRASTRUCTURE ONLY (the oracle of the model path; the product never imports it).
 
 Follows code/lema/model.py:143-363 in hard mode from a state dict with the reference's
 parameter names: embedding; per block pre-RMSNorm, q/k/v projections viewed as

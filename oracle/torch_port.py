@@ -6,7 +6,7 @@ stable argsorts order the 2T events by (code, position, query before key), a cum
 maximum of key positions runs inside each code's segment, and a scatter sends the answers
 back to query positions -- so timing it on the host's cores times the reference's own
 algorithm. `lema_hard_codes` adds the gather and mask of attention.py:157-158. Both run
-on the tensors' device (the CPU baseline times them on the host's cores; the model checker
+on the tensors' device (the CPU baseline times them on the host's cores; the model oracle
 runs them on the GPU).
 """
 from __future__ import annotations

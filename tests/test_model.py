@@ -1,4 +1,4 @@
-"""The model host code and its checker on the CPU: configuration rules, parameter names and
+"""The model host code and its oracle on the CPU: configuration rules, parameter names and
 init (code/lema/model.py:33-82, 258-281), and pins of the functional model oracle."""
 import math
 
