@@ -41,6 +41,13 @@ per second over the timed exchanges. The first call also runs through the refere
 C++ store on the host (`--long-parity-calls` of them): outputs and counts must agree bit for
 bit, and its time is the CPU baseline.
 
+decode_model: single-token decoding of the lm_forward model (24 layers, d_model 1536, 64
+heads, bf16) for a batch of 16 streams after a 4,096-token prompt, through the HBM store with
+worst-case codes (fresh random 64-bit codes every layer and step, the reference's inference
+benchmark hook): one HIP graph replay per token, every layer's store exchange inside it.
+`value` = tokens per second (batch / step time); `roofline` prices the weights and store
+traffic a step must read against HBM peak.
+
 One GPU only: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
@@ -68,7 +75,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="zipf_prefill",
-                    choices=["zipf_prefill", "decode", "lm_forward", "long_context"])
+                    choices=["zipf_prefill", "decode", "lm_forward", "long_context",
+                             "decode_model"])
+    ap.add_argument("--dm-batch", type=int, default=16)
+    ap.add_argument("--dm-prompt", type=int, default=4096)
+    ap.add_argument("--dm-steps", type=int, default=256)
     ap.add_argument("--long-calls", type=int, default=16,
                     help="calls of 2^20 positions of the long_context workload to run")
     ap.add_argument("--long-parity-calls", type=int, default=1,
@@ -559,14 +570,90 @@ def bench_long(a):
     }
 
 
+def bench_decode_model(a):
+    import math
+    import torch
+    from latest_exact_match_attention_amd import build
+    from latest_exact_match_attention_amd.decode import decoder, worst_case_codes
+    from latest_exact_match_attention_amd.model import ModelConfig, Transformer
+
+    if not build.LIB.exists():
+        build.build()
+    cfg = ModelConfig(**LM_CONFIG)
+    B, L, steps = a.dm_batch, a.dm_prompt, a.dm_steps
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Transformer(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model.eval().requires_grad_(False)
+    model.set_hard(True)
+    total = L + steps + a.warmup + 4
+    cache = model.new_cache("hbm", max_cache_len=total, batch=B, max_load=0.7,
+                            codes_hook=worst_case_codes(cfg.depth))
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, 50304, (B, L), generator=g).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        model(prompt[:, :-1], cache=cache, return_logits=False)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        dec = decoder(model, cache, tok=prompt[:, -1:])
+        for _ in range(a.warmup):
+            dec.step(check=False)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            dec.step(check=False)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cache.store.check_full()
+    ms = e0.elapsed_time(e1) / steps
+    P = cfg.depth * B * cfg.num_heads
+    weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    store_bytes = P * DECODE_BYTES_PER_ITEM
+    achieved = (weight_bytes + store_bytes) / (ms * 1e-3) / 1e9
+    return {
+        "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
+        "value": B / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 (GEMMs fp32-accumulated), int64 codes",
+        "data": "synthetic (uniform prompt tokens; random-init weights; worst-case codes)",
+        "config": {"workload": "decode_model", "model": cfg.summary(), "batch": B,
+                   "prompt": L, "store_partitions": P, "store_slots": cache.store.cap,
+                   "store_bytes": cache.nbytes(), "entries_after": cache.entries(),
+                   "prefill_s": round(t_prefill, 3),
+                   "graph": "one replay per token (all 24 layers and their store exchanges)",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm (weights read once per step)", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "kernel": "whole decode step",
+                     "bytes_per_step": weight_bytes + store_bytes},
+        "cpu_baseline": None,
+    }
+
+
 def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (there is no multi-GPU path); got "
               f"--gpus {a.gpus}", file=sys.stderr)
         return 2
-    run = {"decode": bench_decode, "lm_forward": bench_lm,
-           "long_context": bench_long}.get(a.workload, bench_prefill)
+    run = {"decode": bench_decode, "lm_forward": bench_lm, "long_context": bench_long,
+           "decode_model": bench_decode_model}.get(a.workload, bench_prefill)
     out = run(a)
     print(json.dumps(out), flush=True)
     return 0

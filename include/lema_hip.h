@@ -128,6 +128,22 @@ int lema_rmsnorm_bf16(const void* x, const void* d, const void* w, float eps, in
 int lema_cross_entropy_bf16(const void* logits, int64_t rows, int64_t V, int64_t ld,
                             const int64_t* target, float* loss, void* stream);
 
+/* ---- decode-shaped products on the matrix cores (bf16, fp32 accumulation) ---- */
+
+/* y[M, N] = x[M, K] . w[N, K]^T rounded to bf16, for 1 <= M <= 32 rows (a decode step's
+ * tokens). K % 32 == 0; row strides ldx, ldw, ldy in elements (multiples of 8, pointers 16-byte
+ * aligned). Replaces nn.Linear on those shapes (code/lema/model.py:168-179, 85-94). */
+int lema_skinny_gemm_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* The query or key projection straight to codes: z = x . w^T (as above, N = H * d), and
+ * codes[(b * H + h) * T + t] for row m = b * T + t gets bit j = (bf16(z[m, h * d + j]) >= 0).
+ * Replaces project + pack_codes (code/lema/model.py:168-175, code/lema/attention.py:82-97) on
+ * decode shapes; 16 * c must be a multiple of d for some c in 1..4 (d = 24: 48 columns). */
+int lema_skinny_pack_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t M,
+                          int64_t N, int64_t K, int32_t d, int64_t T, void* codes,
+                          int32_t code_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

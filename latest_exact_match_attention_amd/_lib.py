@@ -41,6 +41,9 @@ PROTOTYPES = {
     "lema_swiglu_bf16": ([_p, _p, _p, _i64, _p], ctypes.c_int),
     "lema_rmsnorm_bf16": ([_p, _p, _p, ctypes.c_float, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "lema_cross_entropy_bf16": ([_p, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "lema_skinny_gemm_bf16": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
+    "lema_skinny_pack_bf16": ([_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _i64, _p, _i32, _p],
+                              ctypes.c_int),
     "lema_store_exchange_ws": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p, _p,
                                 _p, _i64, _p], ctypes.c_int),
 }

@@ -19,7 +19,7 @@ import contextlib
 import torch
 
 from .cache import HashStore, LemaCache
-from .model import rms_norm
+from .model import linear, rms_norm
 
 __all__ = ["LemaDecoder", "decoder", "worst_case_codes"]
 
@@ -82,7 +82,7 @@ class LemaDecoder:
             for i in range(L):
                 qc, kc, v = segs[i][0](x)
                 x = segs[i][1](x, views[i].exchange(qc, kc, v, check=False))
-            logits = model.lm_head(rms_norm(x, model.norm_f)[0])
+            logits = linear(rms_norm(x, model.norm_f)[0], model.lm_head)
             self.tok.copy_(choose(logits))
             return logits
 

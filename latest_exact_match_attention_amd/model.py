@@ -86,6 +86,42 @@ def cross_entropy_sum(logits: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
     return loss.sum()
 
 
+SKINNY_ROWS = 32  # products with at most this many token rows run on the skinny MFMA kernel
+
+
+def _skinny(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    K = x.shape[-1]
+    return (_fused(x, weight) and K % 32 == 0 and 0 < x.numel() // K <= SKINNY_ROWS
+            and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def linear(x: torch.Tensor, lin: nn.Linear) -> torch.Tensor:
+    """lin(x); a decode-shaped product (<= 32 rows, bf16) on the skinny MFMA kernel."""
+    if not _skinny(x, lin.weight):
+        return lin(x)
+    K, N = x.shape[-1], lin.weight.shape[0]
+    M = x.numel() // K
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().lema_skinny_gemm_bf16(
+        x.data_ptr(), K, lin.weight.data_ptr(), K, y.data_ptr(), N, M, N, K, _lib.stream_of(x)))
+    return y
+
+
+def project_codes(x: torch.Tensor, lin: nn.Linear, d: int, code_dtype: torch.dtype):
+    """[B, T, dim] -> [B, H, T] codes of lin(x) viewed as H heads of d, or None when the
+    shape is not decode-sized (the caller then projects and packs)."""
+    if not (_skinny(x, lin.weight) and x.dim() == 3
+            and any((16 * c) % d == 0 for c in (1, 2, 3, 4))):
+        return None
+    B, T, K = x.shape
+    N = lin.weight.shape[0]
+    codes = torch.empty((B, N // d, T), dtype=code_dtype, device=x.device)
+    _lib.check(_lib.lib().lema_skinny_pack_bf16(
+        x.data_ptr(), K, lin.weight.data_ptr(), K, B * T, N, K, d, T, codes.data_ptr(),
+        codes.element_size(), _lib.stream_of(x)))
+    return codes
+
+
 ATTN_KINDS = ("lema",)
 POS_KINDS = ("nope",)
 
@@ -151,7 +187,7 @@ class SwiGLU(nn.Module):
         self.down = nn.Linear(dim_ff, dim, bias=False)
 
     def forward(self, x):
-        return self.down(swiglu(self.gate(x), self.up(x)))
+        return linear(swiglu(linear(x, self.gate), linear(x, self.up)), self.down)
 
 
 class Attention(nn.Module):
@@ -175,14 +211,14 @@ class Attention(nn.Module):
         """`[B, T, dim]` -> query and key pre-activations and values, `[B, H, T, d]`."""
         B, T, _ = x.shape
         c = self.cfg
-        zq = self.q_proj(x).view(B, T, c.num_heads, c.d_qk).transpose(1, 2)
-        zk = self.k_proj(x).view(B, T, c.num_kv_heads, c.d_qk).transpose(1, 2)
-        v = self.v_proj(x).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
+        zq = linear(x, self.q_proj).view(B, T, c.num_heads, c.d_qk).transpose(1, 2)
+        zk = linear(x, self.k_proj).view(B, T, c.num_kv_heads, c.d_qk).transpose(1, 2)
+        v = linear(x, self.v_proj).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
         return zq, zk, v
 
     def merge(self, y):
         B, _, T, _ = y.shape
-        return self.o_proj(y.transpose(1, 2).reshape(B, T, -1))
+        return linear(y.transpose(1, 2).reshape(B, T, -1).contiguous(), self.o_proj)
 
     def forward(self, x):
         if not self.hard:
@@ -202,9 +238,18 @@ class Block(nn.Module):
         self.seg = None
 
     def gpu_pre(self, x):
-        """Normalise, project, pack both codes (code/lema/model.py:224-227)."""
-        zq, zk, v = self.attn.project(self.norm1(x))
-        ct = code_dtype_for(self.attn.cfg.d_qk)
+        """Normalise, project, pack both codes (code/lema/model.py:224-227). On decode shapes
+        the q and k projections go straight to codes (skinny MFMA kernel, pack epilogue)."""
+        h = self.norm1(x)
+        at, c = self.attn, self.attn.cfg
+        ct = code_dtype_for(c.d_qk)
+        qc = project_codes(h, at.q_proj, c.d_qk, ct)
+        kc = project_codes(h, at.k_proj, c.d_qk, ct) if qc is not None else None
+        if kc is not None:
+            B, T, _ = h.shape
+            v = linear(h, at.v_proj).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
+            return qc, kc, v
+        zq, zk, v = at.project(h)
         return pack_codes(zq, ct), pack_codes(zk, ct), v
 
     def gpu_post(self, x, got):
@@ -280,7 +325,7 @@ class Transformer(nn.Module):
             x = blk(x, store=(cache.layer(li) if cache is not None else None))
         if cache is not None:
             cache.t += idx.shape[-1]
-        return self.lm_head(rms_norm(x, self.norm_f)[0]) if return_logits else None
+        return linear(rms_norm(x, self.norm_f)[0], self.lm_head) if return_logits else None
 
     def hidden(self, idx):
         """The final normalised hidden states (the input of lm_head), without a cache."""

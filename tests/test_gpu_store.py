@@ -305,3 +305,24 @@ def test_bulk_many_partitions_equals_chunked_path(dev):
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(dumps[0][0], dumps[1][0]) and torch.equal(dumps[0][1], dumps[1][1])
     assert torch.equal(counts[0], counts[1]) and int(counts[0].sum()) == dumps[0][0].numel()
+
+
+@pytest.mark.parametrize("d_v,dtype", [(4, np.float16), (12, np.float16), (2, np.float32)])
+def test_store_value_rows_of_8_byte_pieces(dev, d_v, dtype):
+    """Rows of 8, 24 and 8 bytes (not multiples of 16) take the 8-byte piece copies: decode
+    steps, a chunked call and a long (bulk) call against the dict."""
+    rng = np.random.default_rng(d_v)
+    P = 6
+    vb = d_v * np.dtype(dtype).itemsize
+    store = HashStore(d_v, groups=P, dtype=dtype, capacity=30_000, device=dev)
+    ref = oracle.DictStore(P, vb)
+    for T in (1, 1, 700, 3000, 1):
+        qc = rng.integers(0, 300, P * T)
+        kc = rng.integers(0, 300, P * T)
+        v = rng.integers(0, 256, size=(P * T, vb), dtype=np.uint8)
+        out = torch.empty((P * T, vb), dtype=torch.uint8, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev).to(torch.int32),
+                       torch.from_numpy(kc).to(dev).to(torch.int32),
+                       torch.from_numpy(v).to(dev), out, T, 0)
+        assert np.array_equal(out.cpu().numpy(), ref.exchange(qc, kc, v, T, 0)), T
+    assert np.array_equal(store.counts.numpy(), ref.counts())
