@@ -144,6 +144,30 @@ int lema_skinny_pack_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw
                           int64_t N, int64_t K, int32_t d, int64_t T, void* codes,
                           int32_t code_bytes, void* stream);
 
+/* y = r + x . w^T: the product as in lema_skinny_gemm_bf16, rounded to bf16, then added to the
+ * bf16 residual r [M, ldy] and rounded again (y may alias r). Replaces the MLP's down
+ * projection and the residual add after it, x + mlp(h) (code/lema/model.py:229-232). */
+int lema_skinny_gemm_add_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                              const void* r, void* y, int64_t ldy, int64_t M, int64_t N,
+                              int64_t K, void* stream);
+
+/* A layer's three projections in one launch: the query and key projections (wq, wk: Nqk rows
+ * of H * d) straight to codes as in lema_skinny_pack_bf16, and the value projection (wv: Nv
+ * rows) to v [M, Nv] bf16. All three weights share the row stride ldw. Replaces project +
+ * pack_codes (code/lema/model.py:168-175, 224-227, code/lema/attention.py:82-97) on decode
+ * shapes. */
+int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, const void* wk,
+                         const void* wv, int64_t ldw, int64_t M, int64_t Nqk, int64_t Nv,
+                         int64_t K, int32_t d, int64_t T, void* qcodes, void* kcodes,
+                         int32_t code_bytes, void* v, void* stream);
+
+/* out[M, N] = bf16(bf16(silu(g)) * u), g = bf16(x . wg^T), u = bf16(x . wu^T): the gate and
+ * up projections and SwiGLU's product in one launch (code/lema/model.py:85-94), out row stride
+ * N. */
+int lema_skinny_swiglu_bf16(const void* x, int64_t ldx, const void* wg, const void* wu,
+                            int64_t ldw, int64_t M, int64_t N, int64_t K, void* out,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

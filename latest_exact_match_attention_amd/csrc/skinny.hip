@@ -6,12 +6,16 @@
 // straight from memory (no LDS staging: X is a few KB and stays in L2), and the partial sums
 // are reduced through LDS.
 //
-// Epilogues:
-//   plain  Y rounded to bf16;
-//   pack   the q or k projection straight to codes (code/lema/attention.py:82-97): the block
-//          covers whole heads of d columns, and bit j of a head's code is (bf16(z_j) >= 0),
-//          the sign of the value the unfused path would have stored -- the projection's
-//          output never goes to HBM.
+// Epilogues (a launch can hold up to three weight segments over the same x, e.g. a layer's q,
+// k and v projections):
+//   plain   Y rounded to bf16, optionally added to a bf16 residual (the MLP's down projection
+//           and the residual add of Block.forward, code/lema/model.py:229-232);
+//   pack    the q or k projection straight to codes (code/lema/attention.py:82-97): the block
+//           covers whole heads of d columns, and bit j of a head's code is (bf16(z_j) >= 0),
+//           the sign of the value the unfused path would have stored -- the projection's
+//           output never goes to HBM;
+//   swiglu  silu(x . gate^T) * (x . up^T) with the same bf16 roundings as SwiGLU.forward's
+//           ops (code/lema/model.py:85-94): the block computes 16 columns of both.
 //
 // Operand layout of v_mfma_f32_16x16x32_bf16 (checked on the device): lane l holds A row l%16
 // and B column l%16, k = 8 * (l / 16) + j, j < 8; the result's register r of lane l is row
@@ -28,18 +32,27 @@ constexpr int kSkThreads = 512;
 constexpr int kSkWaves = kSkThreads / 64;
 constexpr int kSkUnroll = 4;  // K-steps of 32 with loads in flight per wavefront
 
+// One weight segment of a launch: its blocks cover N output columns of x . w^T with one
+// epilogue. A launch holds up to three segments sharing x (the q, k and v projections of a
+// layer in one launch).
+enum SkMode : int32_t { kSkPlain = 0, kSkPack = 1, kSkSwiglu = 2 };
+
+struct SkSegment {
+  const uint16_t* w;   // [N, K]
+  const uint16_t* w2;  // swiglu: the up projection [N, K] (w is the gate)
+  void* out;           // plain / swiglu: bf16 [M, ldy]; pack: codes
+  const uint16_t* res; // plain: optional bf16 [M, ldy] residual, out = bf16(res + bf16(sum))
+  int64_t ldy;
+  int32_t N, mode, blocks, code_bytes;
+};
+
 struct SkinnyArgs {
   const uint16_t* x;
-  int64_t ldx;
-  const uint16_t* w;
-  int64_t ldw;
-  uint16_t* y;
-  int64_t ldy;
-  void* codes;
-  int32_t code_bytes;
-  int32_t M, N, K;
-  int32_t d;      // pack: bits per code (one head's columns)
-  int32_t H, T;   // pack: heads per row of Y, positions per stream: row m = (b, t)
+  int64_t ldx, ldw;
+  int32_t M, K;
+  int32_t d, T;  // pack: bits per code (one head), positions per stream (row m = (b, t))
+  int32_t nseg;
+  SkSegment seg[3];
 };
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
@@ -47,17 +60,26 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu) != 0) return 0x7FC0u;
   return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
 }
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 // (bf16(z) >= 0) as a float comparison: -0 -> true, NaN -> false.
 __device__ __forceinline__ bool bf16_nonneg(float z) {
-  return __uint_as_float(f32_to_bf16_bits(z) << 16) >= 0.0f;
+  return bf16_bits_to_f32(f32_to_bf16_bits(z)) >= 0.0f;
 }
 
-template <int MT, int CT, bool PACK>
+// A block owns 16 * CT columns (swiglu: 16 columns of the gate and the same 16 of up).
+template <int MT, int CT>
 __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   __shared__ float part[kSkWaves][MT * 16][CT * 16 + 1];
+  int bid = blockIdx.x, si = 0;
+  while (si + 1 < a.nseg && bid >= a.seg[si].blocks) {
+    bid -= a.seg[si].blocks;
+    ++si;
+  }
+  const SkSegment& sg = a.seg[si];
+  const bool glu = sg.mode == kSkSwiglu;
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int n0 = blockIdx.x * (CT * 16);
+  const int n0 = bid * (glu ? 16 : CT * 16);
   const int ksteps = a.K / 32;
   const int per = (ksteps + kSkWaves - 1) / kSkWaves;
   const int s0 = wave * per;
@@ -68,9 +90,10 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   bool wok[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const int n = n0 + 16 * ct + r16;
-    wok[ct] = n < a.N;
-    wp[ct] = a.w + static_cast<int64_t>(wok[ct] ? n : 0) * a.ldw + kg;
+    const int n = glu ? n0 + r16 : n0 + 16 * ct + r16;
+    wok[ct] = n < sg.N && (!glu || ct < 2);
+    const uint16_t* base = (glu && ct == 1) ? sg.w2 : sg.w;
+    wp[ct] = base + static_cast<int64_t>(wok[ct] ? n : 0) * a.ldw + kg;
   }
   const uint16_t* xp[MT];
   bool xok[MT];
@@ -116,80 +139,117 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   __syncthreads();
 
   constexpr int kRows = MT * 16, kCols = CT * 16;
-  if constexpr (!PACK) {
-    for (int e = threadIdx.x; e < kRows * kCols; e += kSkThreads) {
+  constexpr int kPer = (kRows * kCols + kSkThreads - 1) / kSkThreads;
+  float sums[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = threadIdx.x + i * kSkThreads;
+    sums[i] = 0.f;
+    if (e < kRows * kCols) {
       const int row = e / kCols, col = e - (e / kCols) * kCols;
-      float v = 0.f;
 #pragma unroll
-      for (int wv = 0; wv < kSkWaves; ++wv) v += part[wv][row][col];
-      if (row < a.M && n0 + col < a.N)
-        a.y[static_cast<int64_t>(row) * a.ldy + n0 + col] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+      for (int wv = 0; wv < kSkWaves; ++wv) sums[i] += part[wv][row][col];
     }
-  } else {
-    float sums[(kRows * kCols + kSkThreads - 1) / kSkThreads];
+  }
+  if (sg.mode == kSkPlain) {
+    uint16_t* y = static_cast<uint16_t*>(sg.out);
 #pragma unroll
-    for (int i = 0; i < (kRows * kCols + kSkThreads - 1) / kSkThreads; ++i) {
+    for (int i = 0; i < kPer; ++i) {
       const int e = threadIdx.x + i * kSkThreads;
-      sums[i] = 0.f;
-      if (e < kRows * kCols) {
-        const int row = e / kCols, col = e - (e / kCols) * kCols;
-#pragma unroll
-        for (int wv = 0; wv < kSkWaves; ++wv) sums[i] += part[wv][row][col];
+      const int row = e / kCols, col = e - (e / kCols) * kCols;
+      if (e < kRows * kCols && row < a.M && n0 + col < sg.N) {
+        const int64_t at = static_cast<int64_t>(row) * sg.ldy + n0 + col;
+        uint32_t out = f32_to_bf16_bits(sums[i]);
+        if (sg.res != nullptr) out = f32_to_bf16_bits(bf16_bits_to_f32(sg.res[at]) + bf16_bits_to_f32(out));
+        y[at] = static_cast<uint16_t>(out);
       }
     }
-    __syncthreads();
+    return;
+  }
+  __syncthreads();  // every partial is read: the block's sums go to part[0]
 #pragma unroll
-    for (int i = 0; i < (kRows * kCols + kSkThreads - 1) / kSkThreads; ++i) {
-      const int e = threadIdx.x + i * kSkThreads;
-      if (e < kRows * kCols) part[0][e / kCols][e - (e / kCols) * kCols] = sums[i];
+  for (int i = 0; i < kPer; ++i) {
+    const int e = threadIdx.x + i * kSkThreads;
+    if (e < kRows * kCols) part[0][e / kCols][e - (e / kCols) * kCols] = sums[i];
+  }
+  __syncthreads();
+  if (glu) {  // out = silu(gate) * up, the silu rounded to bf16 first
+    uint16_t* y = static_cast<uint16_t*>(sg.out);
+    for (int e = threadIdx.x; e < kRows * 16; e += kSkThreads) {
+      const int row = e >> 4, c = e & 15;
+      if (row >= a.M || n0 + c >= sg.N) continue;
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(part[0][row][c]));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(part[0][row][16 + c]));
+      const float sl = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.0f + expf(-g))));
+      y[static_cast<int64_t>(row) * sg.ldy + n0 + c] = static_cast<uint16_t>(f32_to_bf16_bits(sl * u));
     }
-    __syncthreads();
-    const int heads = kCols / a.d;  // whole heads per block (checked on the host)
-    for (int e = threadIdx.x; e < kRows * heads; e += kSkThreads) {
-      const int row = e / heads, hh = e - (e / heads) * heads;
-      const int h = n0 / a.d + hh;
-      if (row >= a.M || h >= a.H) continue;
-      uint64_t code = 0;
-      for (int j = 0; j < a.d; ++j)
-        if (bf16_nonneg(part[0][row][hh * a.d + j])) code |= uint64_t(1) << j;
-      const int64_t b = row / a.T, t = row - (row / a.T) * a.T;
-      const int64_t at = (b * a.H + h) * a.T + t;
-      if (a.code_bytes == 4)
-        static_cast<uint32_t*>(a.codes)[at] = static_cast<uint32_t>(code);
-      else
-        static_cast<uint64_t*>(a.codes)[at] = code;
-    }
+    return;
+  }
+  const int heads = kCols / a.d;  // whole heads per block (checked on the host)
+  const int H = sg.N / a.d;
+  for (int e = threadIdx.x; e < kRows * heads; e += kSkThreads) {
+    const int row = e / heads, hh = e - (e / heads) * heads;
+    const int h = n0 / a.d + hh;
+    if (row >= a.M || h >= H) continue;
+    uint64_t code = 0;
+    for (int j = 0; j < a.d; ++j)
+      if (bf16_nonneg(part[0][row][hh * a.d + j])) code |= uint64_t(1) << j;
+    const int64_t b = row / a.T, t = row - (row / a.T) * a.T;
+    const int64_t at = (b * H + h) * a.T + t;
+    if (sg.code_bytes == 4)
+      static_cast<uint32_t*>(sg.out)[at] = static_cast<uint32_t>(code);
+    else
+      static_cast<uint64_t*>(sg.out)[at] = code;
   }
 }
 
-template <int MT, bool PACK>
-int launch_mt(const SkinnyArgs& a, int ct, hipStream_t st) {
-  const int cols = 16 * ct;
-  const dim3 grid((a.N + cols - 1) / cols), block(kSkThreads);
-  switch (ct) {
-    case 1: skinny_kernel<MT, 1, PACK><<<grid, block, 0, st>>>(a); break;
-    case 2: skinny_kernel<MT, 2, PACK><<<grid, block, 0, st>>>(a); break;
-    case 3: skinny_kernel<MT, 3, PACK><<<grid, block, 0, st>>>(a); break;
-    default: skinny_kernel<MT, 4, PACK><<<grid, block, 0, st>>>(a); break;
+template <int CT>
+int launch_skinny(SkinnyArgs& a, hipStream_t st) {
+  int blocks = 0;
+  for (int i = 0; i < a.nseg; ++i) {
+    const int cols = a.seg[i].mode == kSkSwiglu ? 16 : 16 * CT;
+    a.seg[i].blocks = (a.seg[i].N + cols - 1) / cols;
+    blocks += a.seg[i].blocks;
   }
+  const dim3 grid(blocks), block(kSkThreads);
+  if (a.M <= 16)
+    skinny_kernel<1, CT><<<grid, block, 0, st>>>(a);
+  else
+    skinny_kernel<2, CT><<<grid, block, 0, st>>>(a);
   return launch_status("skinny_kernel");
 }
 
-template <bool PACK>
-int launch_skinny(const SkinnyArgs& a, int ct, hipStream_t st) {
-  return a.M <= 16 ? launch_mt<1, PACK>(a, ct, st) : launch_mt<2, PACK>(a, ct, st);
+int launch_ct(SkinnyArgs& a, int ct, hipStream_t st) {
+  switch (ct) {
+    case 1: return launch_skinny<1>(a, st);
+    case 2: return launch_skinny<2>(a, st);
+    case 3: return launch_skinny<3>(a, st);
+    default: return launch_skinny<4>(a, st);
+  }
 }
 
-int check_skinny(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t M, int64_t N,
-                 int64_t K) {
+int check_skinny(const void* x, int64_t ldx, int64_t ldw, int64_t M, int64_t K) {
   LEMA_REQUIRE(M >= 1 && M <= 32, "skinny products take 1..32 rows, got %lld", (long long)M);
-  LEMA_REQUIRE(N >= 1 && N < (int64_t(1) << 30) && K >= 32 && K % 32 == 0 && K < (int64_t(1) << 30),
-               "N=%lld, K=%lld (K a multiple of 32)", (long long)N, (long long)K);
+  LEMA_REQUIRE(K >= 32 && K % 32 == 0 && K < (int64_t(1) << 30), "K=%lld must be a multiple of 32",
+               (long long)K);
   LEMA_REQUIRE(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0,
                "row strides must be >= K and multiples of 8");
-  LEMA_REQUIRE(x != nullptr && w != nullptr && aligned(x, 16) && aligned(w, 16),
-               "x and w must be 16-byte aligned device pointers");
+  LEMA_REQUIRE(x != nullptr && aligned(x, 16), "x must be a 16-byte aligned device pointer");
   return LEMA_OK;
+}
+
+int check_weight(const void* w, int64_t N) {
+  LEMA_REQUIRE(w != nullptr && aligned(w, 16), "weights must be 16-byte aligned device pointers");
+  LEMA_REQUIRE(N >= 1 && N < (int64_t(1) << 30), "N=%lld", (long long)N);
+  return LEMA_OK;
+}
+
+// Columns per block for codes of d bits: the least multiple of 16 (up to 64) holding whole
+// heads, or 0.
+int pack_ct(int32_t d) {
+  for (int c = 1; c <= 4; ++c)
+    if ((16 * c) % d == 0) return c;
+  return 0;
 }
 
 }  // namespace
@@ -201,48 +261,122 @@ extern "C" int lema_skinny_gemm_bf16(const void* x, int64_t ldx, const void* w, 
                                      void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                                      void* stream) {
   clear_error();
-  if (int rc = check_skinny(x, ldx, w, ldw, M, N, K)) return rc;
+  if (int rc = check_skinny(x, ldx, ldw, M, K)) return rc;
+  if (int rc = check_weight(w, N)) return rc;
   LEMA_REQUIRE(y != nullptr && ldy >= N, "bad output");
   SkinnyArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.ldx = ldx;
-  a.w = static_cast<const uint16_t*>(w);
   a.ldw = ldw;
-  a.y = static_cast<uint16_t*>(y);
-  a.ldy = ldy;
   a.M = static_cast<int32_t>(M);
-  a.N = static_cast<int32_t>(N);
   a.K = static_cast<int32_t>(K);
-  return launch_skinny<false>(a, 1, static_cast<hipStream_t>(stream));
+  a.nseg = 1;
+  a.seg[0] = SkSegment{static_cast<const uint16_t*>(w), nullptr, y, nullptr, ldy,
+                       static_cast<int32_t>(N), kSkPlain, 0, 0};
+  return launch_ct(a, 1, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lema_skinny_gemm_add_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                         const void* r, void* y, int64_t ldy, int64_t M, int64_t N,
+                                         int64_t K, void* stream) {
+  clear_error();
+  if (int rc = check_skinny(x, ldx, ldw, M, K)) return rc;
+  if (int rc = check_weight(w, N)) return rc;
+  LEMA_REQUIRE(y != nullptr && r != nullptr && ldy >= N, "bad output or residual");
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.M = static_cast<int32_t>(M);
+  a.K = static_cast<int32_t>(K);
+  a.nseg = 1;
+  a.seg[0] = SkSegment{static_cast<const uint16_t*>(w), nullptr, y,
+                       static_cast<const uint16_t*>(r), ldy, static_cast<int32_t>(N), kSkPlain, 0,
+                       0};
+  return launch_ct(a, 1, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int lema_skinny_pack_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw,
                                      int64_t M, int64_t N, int64_t K, int32_t d, int64_t T,
                                      void* codes, int32_t code_bytes, void* stream) {
   clear_error();
-  if (int rc = check_skinny(x, ldx, w, ldw, M, N, K)) return rc;
+  if (int rc = check_skinny(x, ldx, ldw, M, K)) return rc;
+  if (int rc = check_weight(w, N)) return rc;
   LEMA_REQUIRE(d >= 1 && d <= 64 && N % d == 0, "head width %d must divide N=%lld", d, (long long)N);
   LEMA_REQUIRE(code_bytes == 8 || (code_bytes == 4 && d <= 32), "code_bytes %d for %d-bit codes",
                code_bytes, d);
   LEMA_REQUIRE(T >= 1 && M % T == 0, "rows %lld are not streams x %lld positions", (long long)M,
                (long long)T);
   LEMA_REQUIRE(codes != nullptr && aligned(codes, code_bytes), "bad code pointer");
-  int ct = 0;
-  for (int c = 1; c <= 4 && !ct; ++c)
-    if ((16 * c) % d == 0) ct = c;
+  const int ct = pack_ct(d);
   LEMA_REQUIRE(ct > 0, "head width %d does not tile 16..64 columns", d);
   SkinnyArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.ldx = ldx;
-  a.w = static_cast<const uint16_t*>(w);
   a.ldw = ldw;
-  a.codes = codes;
-  a.code_bytes = code_bytes;
   a.M = static_cast<int32_t>(M);
-  a.N = static_cast<int32_t>(N);
   a.K = static_cast<int32_t>(K);
   a.d = d;
-  a.H = static_cast<int32_t>(N / d);
   a.T = static_cast<int32_t>(T);
-  return launch_skinny<true>(a, ct, static_cast<hipStream_t>(stream));
+  a.nseg = 1;
+  a.seg[0] = SkSegment{static_cast<const uint16_t*>(w), nullptr, codes, nullptr, 0,
+                       static_cast<int32_t>(N), kSkPack, 0, code_bytes};
+  return launch_ct(a, ct, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, const void* wk,
+                                    const void* wv, int64_t ldw, int64_t M, int64_t Nqk,
+                                    int64_t Nv, int64_t K, int32_t d, int64_t T, void* qcodes,
+                                    void* kcodes, int32_t code_bytes, void* v, void* stream) {
+  clear_error();
+  if (int rc = check_skinny(x, ldx, ldw, M, K)) return rc;
+  if (int rc = check_weight(wq, Nqk)) return rc;
+  if (int rc = check_weight(wk, Nqk)) return rc;
+  if (int rc = check_weight(wv, Nv)) return rc;
+  LEMA_REQUIRE(d >= 1 && d <= 64 && Nqk % d == 0, "head width %d must divide %lld", d,
+               (long long)Nqk);
+  LEMA_REQUIRE(code_bytes == 8 || (code_bytes == 4 && d <= 32), "code_bytes %d for %d-bit codes",
+               code_bytes, d);
+  LEMA_REQUIRE(T >= 1 && M % T == 0, "rows %lld are not streams x %lld positions", (long long)M,
+               (long long)T);
+  LEMA_REQUIRE(qcodes && kcodes && aligned(qcodes, code_bytes) && aligned(kcodes, code_bytes) &&
+                   v != nullptr, "bad output pointer");
+  const int ct = pack_ct(d);
+  LEMA_REQUIRE(ct > 0, "head width %d does not tile 16..64 columns", d);
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.M = static_cast<int32_t>(M);
+  a.K = static_cast<int32_t>(K);
+  a.d = d;
+  a.T = static_cast<int32_t>(T);
+  a.nseg = 3;
+  a.seg[0] = SkSegment{static_cast<const uint16_t*>(wq), nullptr, qcodes, nullptr, 0,
+                       static_cast<int32_t>(Nqk), kSkPack, 0, code_bytes};
+  a.seg[1] = SkSegment{static_cast<const uint16_t*>(wk), nullptr, kcodes, nullptr, 0,
+                       static_cast<int32_t>(Nqk), kSkPack, 0, code_bytes};
+  a.seg[2] = SkSegment{static_cast<const uint16_t*>(wv), nullptr, v, nullptr, Nv,
+                       static_cast<int32_t>(Nv), kSkPlain, 0, 0};
+  return launch_ct(a, ct, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lema_skinny_swiglu_bf16(const void* x, int64_t ldx, const void* wg, const void* wu,
+                                       int64_t ldw, int64_t M, int64_t N, int64_t K, void* out,
+                                       void* stream) {
+  clear_error();
+  if (int rc = check_skinny(x, ldx, ldw, M, K)) return rc;
+  if (int rc = check_weight(wg, N)) return rc;
+  if (int rc = check_weight(wu, N)) return rc;
+  LEMA_REQUIRE(out != nullptr, "bad output pointer");
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.M = static_cast<int32_t>(M);
+  a.K = static_cast<int32_t>(K);
+  a.nseg = 1;
+  a.seg[0] = SkSegment{static_cast<const uint16_t*>(wg), static_cast<const uint16_t*>(wu), out,
+                       nullptr, N, static_cast<int32_t>(N), kSkSwiglu, 0, 0};
+  return launch_ct(a, 2, static_cast<hipStream_t>(stream));
 }

@@ -110,8 +110,7 @@ def linear(x: torch.Tensor, lin: nn.Linear) -> torch.Tensor:
 def project_codes(x: torch.Tensor, lin: nn.Linear, d: int, code_dtype: torch.dtype):
     """[B, T, dim] -> [B, H, T] codes of lin(x) viewed as H heads of d, or None when the
     shape is not decode-sized (the caller then projects and packs)."""
-    if not (_skinny(x, lin.weight) and x.dim() == 3
-            and any((16 * c) % d == 0 for c in (1, 2, 3, 4))):
+    if not (_skinny(x, lin.weight) and x.dim() == 3 and _pack_tiles(d)):
         return None
     B, T, K = x.shape
     N = lin.weight.shape[0]
@@ -120,6 +119,32 @@ def project_codes(x: torch.Tensor, lin: nn.Linear, d: int, code_dtype: torch.dty
         x.data_ptr(), K, lin.weight.data_ptr(), K, B * T, N, K, d, T, codes.data_ptr(),
         codes.element_size(), _lib.stream_of(x)))
     return codes
+
+
+def _pack_tiles(d: int) -> bool:
+    return any((16 * c) % d == 0 for c in (1, 2, 3, 4))
+
+
+def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype):
+    """[B, T, dim] -> (qc, kc [B, H, T] codes, v [B, H, T, d_v] view) with all three
+    projections in one launch (skinny MFMA kernel, pack epilogues for q and k), or None when
+    the shape is not decode-sized or the heads differ in count."""
+    c = at.cfg
+    wq, wk, wv = at.q_proj.weight, at.k_proj.weight, at.v_proj.weight
+    if not (_skinny(x, wq) and x.dim() == 3 and wq.shape == wk.shape and _pack_tiles(c.d_qk)
+            and wk.data_ptr() % 16 == 0 and wv.data_ptr() % 16 == 0
+            and wv.dtype == wq.dtype and wv.is_contiguous() and wk.is_contiguous()):
+        return None
+    B, T, K = x.shape
+    Nqk, Nv = wq.shape[0], wv.shape[0]
+    qc = torch.empty((B, Nqk // c.d_qk, T), dtype=code_dtype, device=x.device)
+    kc = torch.empty_like(qc)
+    v = torch.empty((B, T, Nv), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().lema_skinny_qkv_bf16(
+        x.data_ptr(), K, wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), K, B * T, Nqk, Nv, K,
+        c.d_qk, T, qc.data_ptr(), kc.data_ptr(), qc.element_size(), v.data_ptr(),
+        _lib.stream_of(x)))
+    return qc, kc, v.view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
 
 
 ATTN_KINDS = ("lema",)
@@ -186,8 +211,30 @@ class SwiGLU(nn.Module):
         self.up = nn.Linear(dim, dim_ff, bias=False)
         self.down = nn.Linear(dim_ff, dim, bias=False)
 
-    def forward(self, x):
-        return linear(swiglu(linear(x, self.gate), linear(x, self.up)), self.down)
+    def forward(self, x, residual=None):
+        """down(silu(gate(x)) * up(x)), plus `residual` when given (Block's x + mlp(h)). On
+        decode shapes the gate, up and product are one launch and the down projection adds
+        the residual in its epilogue."""
+        g, u, dn = self.gate.weight, self.up.weight, self.down.weight
+        if _skinny(x, g) and g.shape == u.shape and u.data_ptr() % 16 == 0 and u.is_contiguous():
+            K, N = x.shape[-1], g.shape[0]
+            M = x.numel() // K
+            a = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+            _lib.check(_lib.lib().lema_skinny_swiglu_bf16(
+                x.data_ptr(), K, g.data_ptr(), u.data_ptr(), K, M, N, K, a.data_ptr(),
+                _lib.stream_of(x)))
+            if residual is not None and _skinny(a, dn) and residual.is_contiguous() \
+                    and residual.shape == x.shape[:-1] + (dn.shape[0],) \
+                    and residual.dtype == a.dtype and residual.data_ptr() % 16 == 0:
+                y = torch.empty_like(residual)
+                _lib.check(_lib.lib().lema_skinny_gemm_add_bf16(
+                    a.data_ptr(), N, dn.data_ptr(), N, residual.data_ptr(), y.data_ptr(),
+                    dn.shape[0], M, dn.shape[0], N, _lib.stream_of(x)))
+                return y
+        else:
+            a = swiglu(linear(x, self.gate), linear(x, self.up))
+        y = linear(a, self.down)
+        return y if residual is None else residual + y
 
 
 class Attention(nn.Module):
@@ -239,10 +286,14 @@ class Block(nn.Module):
 
     def gpu_pre(self, x):
         """Normalise, project, pack both codes (code/lema/model.py:224-227). On decode shapes
-        the q and k projections go straight to codes (skinny MFMA kernel, pack epilogue)."""
+        the three projections are one launch, q and k going straight to codes (skinny MFMA
+        kernel, pack epilogues)."""
         h = self.norm1(x)
         at, c = self.attn, self.attn.cfg
         ct = code_dtype_for(c.d_qk)
+        fused = project_qkv(h, at, ct)
+        if fused is not None:
+            return fused
         qc = project_codes(h, at.q_proj, c.d_qk, ct)
         kc = project_codes(h, at.k_proj, c.d_qk, ct) if qc is not None else None
         if kc is not None:
@@ -255,7 +306,7 @@ class Block(nn.Module):
     def gpu_post(self, x, got):
         """Merge the retrieved values and finish the layer (code/lema/model.py:229-232)."""
         h, x = rms_norm(x, self.norm2, self.attn.merge(got))
-        return x + self.mlp(h)
+        return self.mlp(h, residual=x)
 
     def forward(self, x, store=None):
         if store is not None:
@@ -263,7 +314,7 @@ class Block(nn.Module):
             qc, kc, v = pre(x)
             return post(x, store.exchange(qc, kc, v))
         h, x = rms_norm(x, self.norm2, self.attn(self.norm1(x)))
-        return x + self.mlp(h)
+        return self.mlp(h, residual=x)
 
 
 class Transformer(nn.Module):

@@ -79,6 +79,24 @@ def test_graph_decoder_with_worst_case_codes(dev):
     assert (c.counts() == 10).all()
 
 
+def test_bf16_token_steps_match_oracle_loss(dev):
+    """bf16 model stepped one token at a time through the HBM cache -- the decode shapes, where
+    the projections, SwiGLU and the residual add run on the skinny MFMA kernels with their
+    fused epilogues -- gives the functional oracle's loss on the whole sequence within 1e-2
+    relative."""
+    geo = dict(vocab_size=512, depth=3, dim=256, num_heads=8, dim_ff=512)
+    m, cfg = make(dev, dtype=torch.bfloat16, **geo)
+    tok = torch.randint(0, 512, (4, 97), device=dev)
+    x, y = tok[:, :-1], tok[:, 1:]
+    with torch.no_grad():
+        c = m.new_cache("hbm", max_cache_len=x.shape[1], batch=x.shape[0])
+        logits = torch.cat([m(x[:, t:t + 1], cache=c) for t in range(x.shape[1])], dim=1)
+        ours = torch.nn.functional.cross_entropy(logits.float().reshape(-1, cfg.vocab_size),
+                                                 y.reshape(-1)).item()
+        want = torch_model.loss(m.state_dict(), cfg, x, y, chunk=96).item()
+        assert abs(ours - want) <= 1e-2 * abs(want), (ours, want)
+
+
 def check_layers(m, cfg, x, sd):
     """Every layer: the exact op on the model's own codes equals the reference's sort-based
     algorithm on them, bit for bit. Layer 0's codes equal the functional oracle's exactly (the

@@ -51,3 +51,76 @@ def test_skinny_pack_codes(dev, d, B, T):
         bits = ((diff.unsqueeze(-1) >> torch.arange(d, device=dev)) & 1).bool()
         assert (z.abs()[bits] < 1e-3).all()
     assert (diff != 0).float().mean() < 0.01
+
+
+def pack(x, w, d, T, ct):
+    M, K = x.shape
+    H = w.shape[0] // d
+    codes = torch.empty((M // T, H, T), dtype=ct, device=x.device)
+    _lib.check(_lib.lib().lema_skinny_pack_bf16(x.data_ptr(), K, w.data_ptr(), K, M, H * d, K, d,
+                                                T, codes.data_ptr(), codes.element_size(),
+                                                _lib.stream_of(x)))
+    return codes
+
+
+@pytest.mark.parametrize("d,Nv", [(24, 1536), (16, 1024), (32, 2048), (8, 40)])
+@pytest.mark.parametrize("B,T", [(16, 1), (4, 3), (1, 1)])
+def test_skinny_qkv_equals_separate_launches(dev, d, Nv, B, T):
+    """The one-launch q/k/v projection gives bit for bit what three launches give (each column
+    is summed in the same order whatever the block's width)."""
+    H, K = 64, 1536
+    g = torch.Generator(device=dev).manual_seed(d * 3 + B)
+    x = torch.randn(B * T, K, device=dev, generator=g).to(torch.bfloat16)
+    wq, wk = ((torch.randn(H * d, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+              for _ in range(2))
+    wv = (torch.randn(Nv, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+    ct = torch.int32 if d <= 32 else torch.int64
+    qc = torch.full((B, H, T), -1, dtype=ct, device=dev)
+    kc = torch.full_like(qc, -1)
+    v = torch.empty((B * T, Nv), dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.lib().lema_skinny_qkv_bf16(
+        x.data_ptr(), K, wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), K, B * T, H * d, Nv, K, d,
+        T, qc.data_ptr(), kc.data_ptr(), qc.element_size(), v.data_ptr(), _lib.stream_of(x)))
+    assert torch.equal(qc, pack(x, wq, d, T, ct))
+    assert torch.equal(kc, pack(x, wk, d, T, ct))
+    assert torch.equal(v.view(torch.int16), skinny(x, wv).view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [1, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(6144, 1536), (40, 64), (4096, 1024)])
+def test_skinny_swiglu_equals_unfused(dev, M, N, K):
+    """gate, up and the SwiGLU product in one launch against the two products and the
+    elementwise kernel (bit for bit), and against fp32 within bf16 roundings."""
+    from latest_exact_match_attention_amd.model import swiglu
+    g = torch.Generator(device=dev).manual_seed(M + N)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    wg, wu = ((torch.randn(N, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+              for _ in range(2))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.lib().lema_skinny_swiglu_bf16(x.data_ptr(), K, wg.data_ptr(), wu.data_ptr(),
+                                                  K, M, N, K, out.data_ptr(), _lib.stream_of(x)))
+    want = swiglu(skinny(x, wg), skinny(x, wu))
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    zg, zu = x.float() @ wg.float().T, x.float() @ wu.float().T
+    ref = torch.nn.functional.silu(zg) * zu
+    assert ((out.float() - ref).abs() <= 2 ** -6 * ref.abs() + 1e-3).all()
+
+
+@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("N,K", [(1536, 6144), (40, 64)])
+def test_skinny_gemm_add_residual(dev, M, N, K):
+    """y = r + x . w^T with the product rounded to bf16 first, as `x + mlp(h)` in bf16; also
+    in place (y aliasing r)."""
+    g = torch.Generator(device=dev).manual_seed(M * 5 + N)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+    r = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+    want = r + skinny(x, w)
+    y = torch.empty_like(r)
+    fn = _lib.lib().lema_skinny_gemm_add_bf16
+    _lib.check(fn(x.data_ptr(), K, w.data_ptr(), K, r.data_ptr(), y.data_ptr(), N, M, N, K,
+                  _lib.stream_of(x)))
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    _lib.check(fn(x.data_ptr(), K, w.data_ptr(), K, r.data_ptr(), r.data_ptr(), N, M, N, K,
+                  _lib.stream_of(x)))
+    assert torch.equal(r.view(torch.int16), want.view(torch.int16))
