@@ -68,6 +68,26 @@ int lema_hard(const void* qc, const void* kc, int32_t code_bytes, const void* v,
               int64_t v_sh, int64_t v_st, void* y, int64_t y_sb, int64_t y_sh, int64_t y_st,
               int32_t miss, void* src, int32_t src_bytes, void* stream);
 
+/* Workspace bytes lema_latest_prev_match_ws and lema_hard_ws use for N rows of T positions:
+ * 8 KB per 1024 positions, 0 for rows of fewer than 64,513 positions (64 chunks of 1024;
+ * shorter rows keep the backward scan, which is faster there, and need none). No reference counterpart: the reference's sort needs no scratch the
+ * caller provides. */
+int64_t lema_resolve_workspace_bytes(int64_t N, int64_t T);
+
+/* lema_latest_prev_match and lema_hard with a workspace (256-byte aligned, at least
+ * lema_resolve_workspace_bytes(N or B*H, T) bytes; NULL when that is 0): a first kernel writes
+ * per chunk of 1024 keys a summary table (latest position per distinct code), and the
+ * resolver looks keys before a chunk up there instead of scanning all of them. Same results,
+ * same reference functions replaced (code/lema/attention.py:100-132, 155-158). */
+int lema_latest_prev_match_ws(const void* qc, const void* kc, int32_t code_bytes, int64_t N,
+                              int64_t T, void* src, int32_t src_bytes, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+int lema_hard_ws(const void* qc, const void* kc, int32_t code_bytes, const void* v,
+                 int32_t dtype, int64_t B, int64_t H, int64_t T, int64_t dv, int64_t v_sb,
+                 int64_t v_sh, int64_t v_st, void* y, int64_t y_sb, int64_t y_sh, int64_t y_st,
+                 int32_t miss, void* src, int32_t src_bytes, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
 /* The gather alone, for given indices: y = v[src] (miss per `miss`).
  * Replaces code/lema/attention.py:157-158. Shapes and strides as in lema_hard;
  * src is contiguous [B*H, T] of src_bytes, every entry in [-1, T).                      */

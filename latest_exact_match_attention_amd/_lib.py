@@ -33,6 +33,11 @@ PROTOTYPES = {
     "lema_latest_prev_match": ([_p, _p, _i32, _i64, _i64, _p, _i32, _p], ctypes.c_int),
     "lema_hard": ([_p, _p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64,
                    _i64, _i64, _i32, _p, _i32, _p], ctypes.c_int),
+    "lema_latest_prev_match_ws": ([_p, _p, _i32, _i64, _i64, _p, _i32, _p, _i64, _p],
+                                  ctypes.c_int),
+    "lema_resolve_workspace_bytes": ([_i64, _i64], ctypes.c_int64),
+    "lema_hard_ws": ([_p, _p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,
+                      _i64, _i64, _i64, _i32, _p, _i32, _p, _i64, _p], ctypes.c_int),
     "lema_gather": ([_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i32, _p, _i64,
                      _i64, _i64, _i32, _p], ctypes.c_int),
     "lema_store_exchange": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p, _p, _p],

@@ -12,6 +12,7 @@ import torch
 from . import _lib
 
 __all__ = ["pack_codes", "latest_prev_match", "lema_hard", "lema_from_codes", "gather_values",
+           "resolve_workspace",
            "code_dtype_for"]
 
 
@@ -90,10 +91,19 @@ def latest_prev_match(qc: torch.Tensor, kc: torch.Tensor,
     src = torch.empty((N, T), dtype=out_dtype, device=qc.device)
     if src.numel() == 0:
         return src
-    _lib.check(_lib.lib().lema_latest_prev_match(
+    ws = resolve_workspace(N, T, qc.device)
+    _lib.check(_lib.lib().lema_latest_prev_match_ws(
         qc.data_ptr(), kc.data_ptr(), cb, N, T, src.data_ptr(), src.element_size(),
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         _lib.stream_of(qc)))
     return src
+
+
+def resolve_workspace(N: int, T: int, device) -> torch.Tensor | None:
+    """Scratch for the chunk summaries of N rows of T positions (None when rows are short
+    enough for the backward scan): 8 KB per 1024 positions."""
+    n = _lib.lib().lema_resolve_workspace_bytes(N, T)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
 
 
 def _value4(v: torch.Tensor) -> torch.Tensor:
@@ -122,17 +132,22 @@ def _hard_forward(qc: torch.Tensor, kc: torch.Tensor, v: torch.Tensor,
 
 
 def launch_hard(qc: torch.Tensor, kc: torch.Tensor, v: torch.Tensor, y: torch.Tensor,
-                src: torch.Tensor | None = None, miss: int = _lib.MISS_DENSE) -> None:
-    """Enqueue the fused kernel on preallocated buffers (no allocation, graph-capturable):
-    qc, kc contiguous [B*H, T] (int32 or int64), v and y [B, H, T, dv] with a contiguous
-    last dim, src None or contiguous int32/int64 [B, H, T]."""
+                src: torch.Tensor | None = None, miss: int = _lib.MISS_DENSE,
+                workspace: torch.Tensor | None = None) -> None:
+    """Enqueue the fused kernels on preallocated buffers: qc, kc contiguous [B*H, T] (int32 or
+    int64), v and y [B, H, T, dv] with a contiguous last dim, src None or contiguous
+    int32/int64 [B, H, T], workspace None or `resolve_workspace(B*H, T)` (allocated here when
+    needed and not given; pass it to keep the call allocation-free)."""
     B, H, T, dv = v.shape
     cb = qc.element_size()
-    _lib.check(_lib.lib().lema_hard(
+    ws = workspace if workspace is not None else resolve_workspace(B * H, T, v.device)
+    _lib.check(_lib.lib().lema_hard_ws(
         qc.data_ptr(), kc.data_ptr(), cb, v.data_ptr(), _lib.DTYPE_CODE[v.dtype], B, H, T, dv,
         v.stride(0), v.stride(1), v.stride(2), y.data_ptr(), y.stride(0), y.stride(1),
         y.stride(2), miss, src.data_ptr() if src is not None else None,
-        src.element_size() if src is not None else 4, _lib.stream_of(v)))
+        src.element_size() if src is not None else 4,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        _lib.stream_of(v)))
 
 
 def lema_from_codes(qc: torch.Tensor, kc: torch.Tensor, v: torch.Tensor,

@@ -18,6 +18,14 @@
 // no scratch memory. Step (c) costs O(T^2 / 1024) lookups per row, reading the row's key
 // codes from L2 with 16-byte loads one batch ahead; at T = 16k that is 7.5 per query.
 //
+// With a workspace (the _ws entry points, rows of at least 64 chunks), step (c) instead reads
+// chunk summaries written by summary_kernel just before: per full chunk, a 2048-slot table of
+// (fingerprint, latest position) per distinct key code. Only the query codes with no earlier
+// key in their own chunk (about 300 of 1024 positions' codes on Zipf data) probe the earlier
+// chunks' tables, latest first, 8 chunks per round trip, and every candidate is confirmed
+// against the key code itself, so the answer stays exact; the LDS work of step (c) drops from
+// O(T / 1024) lookups per query to none.
+//
 // The gather is fused: after resolving, the workgroup copies its 1024 value rows
 // v[src] -> y in 16-byte pieces, consecutive threads on consecutive pieces, so both the reads
 // of each source row and the (non-temporal) writes of y are coalesced.
@@ -31,20 +39,34 @@ namespace lema {
 namespace {
 
 // One workgroup (256 threads) per (row, chunk): resolve, then (VEC > 0) gather the chunk's
-// value rows. XCD-aware work mapping: every chunk of row r runs on XCD r % 8, which then keeps
-// that row's key codes and value rows in its own L2; the heaviest chunks (latest) go first.
-template <typename CodeT, int VEC>
+// value rows. XCD-aware work mapping: workgroup b runs on XCD b % 8. When the rows come in
+// whole groups of 64, rows 8g..8g+7 belong to XCD g % 8 and its workgroups take one chunk of
+// all 8 rows back to back, latest chunks first: the 8 rows' key codes and value rows share
+// that XCD's L2, and where y interleaves the rows (y viewed from [B, T, H * dv]) their pieces
+// of each output line are written close together in the same L2 (measured: 116 -> 112 us on
+// B8 H16 T16384 Zipf codes; 307 -> 172 us, with the filter, on a language-model layer of B4
+// H64 T16384 d 24). Otherwise every chunk of row r runs on XCD r % 8, latest chunks first.
+template <typename CodeT, int VEC, bool kSumm>
 __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
   __shared__ ResolveLds<CodeT> s;
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
   const int k = bid / kNumXcd;
-  const int chunk = a.nchunks - 1 - (k % a.nchunks);
-  const int64_t row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
+  int chunk;
+  int64_t row;
+  if (a.group) {
+    const int per = kNumXcd * a.nchunks;
+    chunk = a.nchunks - 1 - (k % per) / kNumXcd;
+    row = (static_cast<int64_t>(k / per) * kNumXcd + xcd) * kNumXcd + (k % per) % kNumXcd;
+  } else {
+    chunk = a.nchunks - 1 - (k % a.nchunks);
+    row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
+  }
   if (row >= a.N) return;
   const int t = threadIdx.x;
   int32_t src[kPer];
-  resolve_chunk(s, a, row, chunk, t, [] { __syncthreads(); }, src);
+  auto bar = [] { __syncthreads(); };
+  resolve_chunk<CodeT, decltype(bar), kSumm>(s, a, row, chunk, t, bar, src);
   if constexpr (VEC > 0) {
     int32_t* srcs = reinterpret_cast<int32_t*>(s.mbits);  // the masks are dead now
     __syncthreads();
@@ -56,6 +78,97 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
     gather_rows<VEC, 8, LEMA_GATHER_INFLIGHT>(a.g, row, c0, n_here, t, kThreads,
                             [&](uint32_t r) -> int64_t { return srcs[r]; });
   }
+}
+
+// One workgroup per (row, full chunk except the row's last): the chunk's summary table. The
+// LDS table is keyed by the whole code (the all-ones code, its empty marker, is kept apart);
+// each key raises its code's latest position with an atomicMax, and the table's image goes
+// to HBM with the fingerprints in place of the codes.
+// Shorter rows keep the backward scan: its LDS lookups cost O(T) per query, but the summaries'
+// extra kernel and the probes' round trips to L2 cost more until about 64 chunks (measured at
+// 2M queries: scan 124 vs 146 us at T = 16384, 192 vs 188 us at 65536, 251 vs 227 at 131072).
+constexpr int kSummaryMinChunks = 64;
+
+template <typename CodeT>
+__global__ __launch_bounds__(kThreads) void summary_kernel(ResolveArgs a) {
+  __shared__ __attribute__((aligned(16))) CodeT code[kSumSlots];  // read 4 slots at a time
+  __shared__ int32_t last[kSumSlots];
+  __shared__ int32_t sent_last;
+  const int per = a.nchunks - 1;
+  const int bid = blockIdx.x;
+  const int xcd = bid % kNumXcd;
+  const int k = bid / kNumXcd;
+  const int chunk = k % per;
+  const int64_t row = static_cast<int64_t>(k / per) * kNumXcd + xcd;
+  if (row >= a.N) return;
+  const int t = threadIdx.x;
+  const CodeT SENT = sentinel<CodeT>();
+  const CodeT* krow = static_cast<const CodeT*>(a.kc) + row * a.T + chunk * kChunk;
+  CodeT kk[kPer];
+  int o[kPer];
+  if (a.kvec) {  // 4 consecutive codes per thread, 16-byte aligned
+    if constexpr (sizeof(CodeT) == 4) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(krow + 4 * t);
+      kk[0] = v.x; kk[1] = v.y; kk[2] = v.z; kk[3] = v.w;
+    } else {
+      const u32x4 v0 = *reinterpret_cast<const u32x4*>(krow + 4 * t);
+      const u32x4 v1 = *reinterpret_cast<const u32x4*>(krow + 4 * t + 2);
+      kk[0] = (uint64_t(v0.y) << 32) | v0.x; kk[1] = (uint64_t(v0.w) << 32) | v0.z;
+      kk[2] = (uint64_t(v1.y) << 32) | v1.x; kk[3] = (uint64_t(v1.w) << 32) | v1.z;
+    }
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) o[p] = 4 * t + p;
+  } else {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      o[p] = p * kThreads + t;
+      kk[p] = krow[o[p]];
+    }
+  }
+  for (int x = t; x < kSumSlots; x += kThreads) {
+    code[x] = SENT;
+    last[x] = -1;
+  }
+  if (t == 0) sent_last = -1;
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < kPer; ++p) {
+    if (kk[p] == SENT) {
+      atomicMax(&sent_last, o[p]);
+      continue;
+    }
+    bool ins;
+    const int sl = table_claim<CodeT, kSumBuckets>(code, kk[p], SENT, bucket_of<kSumBuckets>(fold(kk[p])), ins);
+    atomicMax(&last[sl], o[p]);
+  }
+  __syncthreads();
+  uint32_t* tab = a.summ_tab + (row * a.nchunks + chunk) * kSumSlots;
+  for (int b = t; b < kSumBuckets; b += kThreads) {
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const CodeT c = code[4 * b + i];
+      e[i] = c == SENT ? kSumEmpty
+                       : (fingerprint(fold(c)) << 10) | static_cast<uint32_t>(last[4 * b + i]);
+    }
+    *reinterpret_cast<u32x4*>(tab + 4 * b) = u32x4{e[0], e[1], e[2], e[3]};
+  }
+  if (t == 0) a.summ_sent[row * a.nchunks + chunk] = sent_last;
+}
+
+// Workspace of the summary path: the tables, then the all-ones code's positions.
+struct SummaryLayout {
+  int64_t tab_bytes, sent_off, bytes;
+};
+
+SummaryLayout summary_layout(int64_t N, int64_t T) {
+  SummaryLayout L{0, 0, 0};
+  const int64_t nchunks = (T + kChunk - 1) / kChunk;
+  if (N <= 0 || nchunks < kSummaryMinChunks) return L;
+  L.tab_bytes = N * nchunks * kSumSlots * 4;
+  L.sent_off = (L.tab_bytes + 255) / 256 * 256;
+  L.bytes = L.sent_off + (N * nchunks * 4 + 255) / 256 * 256;
+  return L;
 }
 
 // Standalone gather for given indices: one workgroup per (row, 1024 positions).
@@ -130,21 +243,39 @@ int fill_gather(GatherArgs& g, const void* v, int32_t dtype, int64_t H, int64_t 
     if (g.pieces == (1u << l)) g.plog = l;
   g.miss = miss;
   g.dtype = dtype;
+  g.nt = y_st == dv;  // rows of y adjacent: stream them out; else let L2 merge the pieces
   *vec_out = vec;
   return LEMA_OK;
 }
 
+template <typename CodeT, bool kSumm>
+int launch_vec(ResolveArgs& a, int vec, int64_t grid, hipStream_t st);
+
 template <typename CodeT>
 int launch_resolve(ResolveArgs& a, int vec, hipStream_t st) {
   a.kvec = (aligned(a.kc, 16) && (a.T * static_cast<int64_t>(sizeof(CodeT))) % 16 == 0) ? 1 : 0;
-  const int64_t grid = (a.N + kNumXcd - 1) / kNumXcd * kNumXcd * a.nchunks;
+  a.group = a.N % 64 == 0;  // 8 whole groups of 8 rows per XCD at least: the grouped order
+  const int64_t groups = (a.N + kNumXcd - 1) / kNumXcd;
+  const int64_t grid = a.group ? (groups + kNumXcd - 1) / kNumXcd * kNumXcd * kNumXcd * a.nchunks
+                               : (a.N + kNumXcd - 1) / kNumXcd * kNumXcd * a.nchunks;
   LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows x chunks (%lld)", (long long)grid);
+  if (a.summ_tab != nullptr) {
+    const int64_t sgrid = (a.N + kNumXcd - 1) / kNumXcd * kNumXcd * (a.nchunks - 1);
+    summary_kernel<CodeT><<<dim3(sgrid), dim3(kThreads), 0, st>>>(a);
+    if (int rc = launch_status("summary_kernel")) return rc;
+    return launch_vec<CodeT, true>(a, vec, grid, st);
+  }
+  return launch_vec<CodeT, false>(a, vec, grid, st);
+}
+
+template <typename CodeT, bool kSumm>
+int launch_vec(ResolveArgs& a, int vec, int64_t grid, hipStream_t st) {
   switch (vec) {
-    case 0: resolve_kernel<CodeT, 0><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 16: resolve_kernel<CodeT, 16><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 8: resolve_kernel<CodeT, 8><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 4: resolve_kernel<CodeT, 4><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 2: resolve_kernel<CodeT, 2><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 0: resolve_kernel<CodeT, 0, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 16: resolve_kernel<CodeT, 16, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 8: resolve_kernel<CodeT, 8, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 4: resolve_kernel<CodeT, 4, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 2: resolve_kernel<CodeT, 2, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
     default: set_error("internal: piece size %d", vec); return LEMA_BAD_ARG;
   }
   return launch_status("resolve_kernel");
@@ -163,12 +294,24 @@ int check_rows(const void* qc, const void* kc, int32_t code_bytes, int64_t N, in
 }  // namespace
 }  // namespace lema
 
-using namespace lema;
+namespace lema {
+namespace {
 
-extern "C" int lema_latest_prev_match(const void* qc, const void* kc, int32_t code_bytes,
-                                      int64_t N, int64_t T, void* src, int32_t src_bytes,
-                                      void* stream) {
-  clear_error();
+// Points a at the summaries in the caller's workspace when the row length calls for them.
+int use_workspace(ResolveArgs& a, void* workspace, int64_t ws_bytes) {
+  const SummaryLayout L = summary_layout(a.N, a.T);
+  if (L.bytes == 0) return LEMA_OK;
+  LEMA_REQUIRE(workspace != nullptr && aligned(workspace, 256) && ws_bytes >= L.bytes,
+               "workspace of %lld bytes (256-byte aligned) needed, got %lld", (long long)L.bytes,
+               (long long)ws_bytes);
+  a.summ_tab = static_cast<uint32_t*>(workspace);
+  a.summ_sent = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + L.sent_off);
+  return LEMA_OK;
+}
+
+int latest_prev_match(const void* qc, const void* kc, int32_t code_bytes, int64_t N, int64_t T,
+                      void* src, int32_t src_bytes, void* workspace, int64_t ws_bytes,
+                      hipStream_t st) {
   if (int rc = check_rows(qc, kc, code_bytes, N, T)) return rc;
   LEMA_REQUIRE(src_bytes == 4 || src_bytes == 8, "src_bytes must be 4 or 8, got %d", src_bytes);
   LEMA_REQUIRE(N * T == 0 || (src != nullptr && aligned(src, src_bytes)), "bad src pointer");
@@ -181,16 +324,15 @@ extern "C" int lema_latest_prev_match(const void* qc, const void* kc, int32_t co
   a.nchunks = static_cast<int32_t>((T + kChunk - 1) / kChunk);
   a.src = src;
   a.src_bytes = src_bytes;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (workspace != nullptr)
+    if (int rc = use_workspace(a, workspace, ws_bytes)) return rc;
   return code_bytes == 4 ? launch_resolve<uint32_t>(a, 0, st) : launch_resolve<uint64_t>(a, 0, st);
 }
 
-extern "C" int lema_hard(const void* qc, const void* kc, int32_t code_bytes, const void* v,
-                         int32_t dtype, int64_t B, int64_t H, int64_t T, int64_t dv,
-                         int64_t v_sb, int64_t v_sh, int64_t v_st, void* y, int64_t y_sb,
-                         int64_t y_sh, int64_t y_st, int32_t miss, void* src,
-                         int32_t src_bytes, void* stream) {
-  clear_error();
+int hard(const void* qc, const void* kc, int32_t code_bytes, const void* v, int32_t dtype,
+         int64_t B, int64_t H, int64_t T, int64_t dv, int64_t v_sb, int64_t v_sh, int64_t v_st,
+         void* y, int64_t y_sb, int64_t y_sh, int64_t y_st, int32_t miss, void* src,
+         int32_t src_bytes, void* workspace, int64_t ws_bytes, hipStream_t st) {
   LEMA_REQUIRE(B >= 0 && H >= 0, "negative shape B=%lld H=%lld", (long long)B, (long long)H);
   const int64_t N = B * H;
   if (int rc = check_rows(qc, kc, code_bytes, N, T)) return rc;
@@ -210,8 +352,55 @@ extern "C" int lema_hard(const void* qc, const void* kc, int32_t code_bytes, con
   a.nchunks = static_cast<int32_t>((T + kChunk - 1) / kChunk);
   a.src = src;
   a.src_bytes = src_bytes;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (workspace != nullptr)
+    if (int rc = use_workspace(a, workspace, ws_bytes)) return rc;
   return code_bytes == 4 ? launch_resolve<uint32_t>(a, vec, st) : launch_resolve<uint64_t>(a, vec, st);
+}
+
+}  // namespace
+}  // namespace lema
+
+using namespace lema;
+
+extern "C" int lema_latest_prev_match(const void* qc, const void* kc, int32_t code_bytes,
+                                      int64_t N, int64_t T, void* src, int32_t src_bytes,
+                                      void* stream) {
+  clear_error();
+  return latest_prev_match(qc, kc, code_bytes, N, T, src, src_bytes, nullptr, 0,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lema_latest_prev_match_ws(const void* qc, const void* kc, int32_t code_bytes,
+                                         int64_t N, int64_t T, void* src, int32_t src_bytes,
+                                         void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return latest_prev_match(qc, kc, code_bytes, N, T, src, src_bytes, workspace, workspace_bytes,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t lema_resolve_workspace_bytes(int64_t N, int64_t T) {
+  return summary_layout(N, T).bytes;
+}
+
+extern "C" int lema_hard(const void* qc, const void* kc, int32_t code_bytes, const void* v,
+                         int32_t dtype, int64_t B, int64_t H, int64_t T, int64_t dv,
+                         int64_t v_sb, int64_t v_sh, int64_t v_st, void* y, int64_t y_sb,
+                         int64_t y_sh, int64_t y_st, int32_t miss, void* src,
+                         int32_t src_bytes, void* stream) {
+  clear_error();
+  return hard(qc, kc, code_bytes, v, dtype, B, H, T, dv, v_sb, v_sh, v_st, y, y_sb, y_sh, y_st,
+              miss, src, src_bytes, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lema_hard_ws(const void* qc, const void* kc, int32_t code_bytes, const void* v,
+                            int32_t dtype, int64_t B, int64_t H, int64_t T, int64_t dv,
+                            int64_t v_sb, int64_t v_sh, int64_t v_st, void* y, int64_t y_sb,
+                            int64_t y_sh, int64_t y_st, int32_t miss, void* src,
+                            int32_t src_bytes, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+  clear_error();
+  return hard(qc, kc, code_bytes, v, dtype, B, H, T, dv, v_sb, v_sh, v_st, y, y_sb, y_sh, y_st,
+              miss, src, src_bytes, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int lema_gather(const void* v, int32_t dtype, int64_t B, int64_t H, int64_t T,

@@ -2,6 +2,8 @@
 // (resolve.hip) and the store's in-chunk resolution (store.hip). The design is described at the
 // top of resolve.hip.
 #pragma once
+#include <type_traits>
+
 #include "lema_internal.h"
 
 namespace lema {
@@ -41,9 +43,13 @@ constexpr int kChunk = kThreads * kPer;
 #ifndef LEMA_RESOLVE_SLOTS
 #define LEMA_RESOLVE_SLOTS 2048
 #endif
+#ifndef LEMA_RESOLVE_PREFETCH
+#define LEMA_RESOLVE_PREFETCH 1
+#endif
 #ifndef LEMA_RESOLVE_MAP_SLOTS
 #define LEMA_RESOLVE_MAP_SLOTS 1536
 #endif
+constexpr int kPrefetch = LEMA_RESOLVE_PREFETCH;  // key batches loaded ahead of the lookups
 constexpr int kSlots = LEMA_RESOLVE_SLOTS;  // query-code table: at most kChunk codes
 constexpr int kBuckets = kSlots / 4;
 constexpr int kMapSlots = LEMA_RESOLVE_MAP_SLOTS;  // (code slot, word) -> lane mask: at most
@@ -52,6 +58,19 @@ static_assert(kSlots > kChunk && kSlots % 4 == 0 && kMapSlots > kChunk && kMapSl
               "tables must keep free slots");
 constexpr uint32_t kMapEmpty = 0xFFFFFFFFu;
 static_assert(kChunk / 64 <= 16, "word summary is a 16-bit mask");
+
+// A one-hash bit filter of the chunk's query codes (8192 bits for at most 1024 codes): a key
+// whose bit is clear carries no query code, and skips the table lookup. Keys of codes that
+// seldom repeat (pre-activation codes of a language model) then cost one 4-byte LDS read
+// each. LEMA_RESOLVE_FILTER: 0 never, 1 always, 2 in chunks of more than kFilterMinCodes
+// distinct query codes (on Zipf-distributed codes, ~370 per chunk, the filter passes most
+// keys and only adds a read).
+#ifndef LEMA_RESOLVE_FILTER
+#define LEMA_RESOLVE_FILTER 2
+#endif
+constexpr int kFilterWords = 256;
+constexpr int kFilterMinCodes = 512;  // used by chunks with more distinct query codes than this
+__device__ __forceinline__ uint32_t filter_hash(uint32_t h) { return (h * 0x2C1B3C6Du) >> 19; }
 
 template <typename CodeT>
 struct ResolveLds {
@@ -62,7 +81,10 @@ struct ResolveLds {
                               // [kSlots] here and in summ belongs to the sentinel code itself
   alignas(4) uint16_t summ[kSlots + 2];  // bit w: word w of the chunk holds a key with this
                                          // code; updated as 32-bit pairs
+  uint32_t qbits[kFilterWords];  // bit filter_hash(c) set for every query code c of the chunk
   int32_t sent_used;
+  int32_t nq;     // distinct query codes of the chunk (the all-ones code aside)
+  int32_t nneed;  // query codes that need their latest key before the chunk (summary path)
 };
 
 // The 4 slots of bucket b, one (u32 codes) or two (u64 codes) 16-byte LDS reads.
@@ -142,6 +164,8 @@ struct GatherArgs {
   int32_t plog;     // log2(pieces) when pieces is a power of two <= 64, else -1
   int32_t miss;
   int32_t dtype;
+  int32_t nt;  // non-temporal stores of y (rows of y adjacent); plain stores let L2 merge the
+               // pieces of interleaved rows (y viewed from [B, T, H * dv]) into whole lines
 };
 
 struct ResolveArgs {
@@ -152,8 +176,99 @@ struct ResolveArgs {
   int32_t kvec;  // key rows allow 16-byte loads of 4 consecutive codes
   void* src;     // optional
   int32_t src_bytes;
+  // Chunk summaries (optional): per (row, chunk) a table of kSumSlots entries, one per
+  // distinct key code of the chunk, and the latest position of the all-ones code. With them,
+  // keys before a chunk are found by probing the summaries of earlier chunks instead of
+  // scanning every earlier key.
+  uint32_t* summ_tab;
+  int32_t* summ_sent;
+  int32_t group;  // workgroup order: 8 consecutive rows per XCD, one chunk of all 8 in a row
   GatherArgs g;
 };
+
+// ------------------------------------------------------------------ chunk summaries
+// Entry of a summary table: (fingerprint << 10) | position in the chunk, kSumEmpty = free.
+// The table is the image of an LDS table keyed by the whole code (4-slot buckets from
+// bucket_of, linear probing), so a lookup visits the code's slot before any free slot. The
+// fingerprint only filters: every candidate is confirmed against the key code itself.
+constexpr int kSumSlots = 2048;
+constexpr int kSumBuckets = kSumSlots / 4;
+constexpr uint32_t kSumEmpty = 0xFFFFFFFFu;
+static_assert(kSumSlots > 1024, "a summary table keeps free slots");
+
+// 22-bit fingerprint: the MurmurHash3 32-bit finaliser of the folded code, top bits; never
+// the all-ones value (that entry would read as free).
+__device__ __forceinline__ uint32_t fingerprint(uint32_t h) {
+  h ^= h >> 16;
+  h *= 0x85EBCA6Bu;
+  h ^= h >> 13;
+  h *= 0xC2B2AE35u;
+  h ^= h >> 16;
+  const uint32_t f = h >> 10;
+  return f == 0x3FFFFFu ? 0x3FFFFEu : f;
+}
+
+// Latest position of code x in full chunk cc of a row (krow = the row's keys), or -1, from
+// the chunk's summary table tab, whose bucket b0 is already in e.
+template <typename CodeT>
+__device__ __forceinline__ int32_t summary_probe(const uint32_t* tab, const CodeT* krow, int cc,
+                                                 CodeT x, uint32_t fp, int b0, u32x4 e) {
+  int b = b0;
+  for (;;) {
+    const uint32_t ent[4] = {e.x, e.y, e.z, e.w};
+    bool open = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (ent[i] == kSumEmpty) {
+        open = true;
+      } else if ((ent[i] >> 10) == fp) {
+        const int32_t j = cc * 1024 + static_cast<int32_t>(ent[i] & 1023u);
+        if (krow[j] == x) return j;
+      }
+    }
+    if (open) return -1;
+    b = b + 1 == kSumBuckets ? 0 : b + 1;
+    e = *reinterpret_cast<const u32x4*>(tab + 4 * b);
+  }
+}
+
+// Latest key position before chunk `chunk` of row `row` for code x (sent: x is the all-ones
+// code), or -1: the summaries of the earlier chunks are probed latest first, 8 at a time
+// with their first buckets loaded together.
+template <typename CodeT>
+__device__ __forceinline__ int32_t before_chunk(const ResolveArgs& a, int64_t row, int chunk, CodeT x, bool sent) {
+  constexpr int kAhead = 8;
+  const int64_t rc = row * a.nchunks;
+  if (sent) {
+    for (int cb = chunk - 1; cb >= 0; cb -= kAhead) {
+      int32_t v[kAhead];
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i) v[i] = cb - i >= 0 ? a.summ_sent[rc + cb - i] : -1;
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i)
+        if (v[i] >= 0) return (cb - i) * 1024 + v[i];
+    }
+    return -1;
+  }
+  const CodeT* krow = static_cast<const CodeT*>(a.kc) + row * a.T;
+  const uint32_t fp = fingerprint(fold(x));
+  const int b0 = bucket_of<kSumBuckets>(fold(x));
+  for (int cb = chunk - 1; cb >= 0; cb -= kAhead) {
+    u32x4 e[kAhead];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i)
+      e[i] = cb - i >= 0 ? *reinterpret_cast<const u32x4*>(a.summ_tab + (rc + cb - i) * kSumSlots + 4 * b0)
+                         : u32x4{kSumEmpty, kSumEmpty, kSumEmpty, kSumEmpty};
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) {
+      if (cb - i < 0) break;
+      const int32_t j = summary_probe(a.summ_tab + (rc + cb - i) * kSumSlots, krow, cb - i, x,
+                                      fp, b0, e[i]);
+      if (j >= 0) return j;
+    }
+  }
+  return -1;
+}
 
 // ------------------------------------------------------------------ miss fill (dense path)
 // y = v[row, 0] * 0 in the value dtype: a zero with v's sign, a quiet NaN for NaN (payload
@@ -182,8 +297,12 @@ template <>
 struct Piece<16> {
   typedef u32x4 T;
   static __device__ __forceinline__ T load(const uint8_t* p) { return *reinterpret_cast<const T*>(p); }
+  template <bool NT>
   static __device__ __forceinline__ void store(uint8_t* p, T v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    if constexpr (NT)
+      __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    else
+      *reinterpret_cast<T*>(p) = v;
   }
   static __device__ __forceinline__ T zero() { return T{0u, 0u, 0u, 0u}; }
   static __device__ __forceinline__ T miss(T v, int32_t d) {
@@ -194,8 +313,12 @@ template <>
 struct Piece<8> {
   typedef u32x2 T;
   static __device__ __forceinline__ T load(const uint8_t* p) { return *reinterpret_cast<const T*>(p); }
+  template <bool NT>
   static __device__ __forceinline__ void store(uint8_t* p, T v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    if constexpr (NT)
+      __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    else
+      *reinterpret_cast<T*>(p) = v;
   }
   static __device__ __forceinline__ T zero() { return T{0u, 0u}; }
   static __device__ __forceinline__ T miss(T v, int32_t d) { return T{miss_word(v.x, d), miss_word(v.y, d)}; }
@@ -204,8 +327,12 @@ template <>
 struct Piece<4> {
   typedef uint32_t T;
   static __device__ __forceinline__ T load(const uint8_t* p) { return *reinterpret_cast<const T*>(p); }
+  template <bool NT>
   static __device__ __forceinline__ void store(uint8_t* p, T v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    if constexpr (NT)
+      __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    else
+      *reinterpret_cast<T*>(p) = v;
   }
   static __device__ __forceinline__ T zero() { return 0u; }
   static __device__ __forceinline__ T miss(T v, int32_t d) { return miss_word(v, d); }
@@ -214,8 +341,12 @@ template <>
 struct Piece<2> {
   typedef uint16_t T;
   static __device__ __forceinline__ T load(const uint8_t* p) { return *reinterpret_cast<const T*>(p); }
+  template <bool NT>
   static __device__ __forceinline__ void store(uint8_t* p, T v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    if constexpr (NT)
+      __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+    else
+      *reinterpret_cast<T*>(p) = v;
   }
   static __device__ __forceinline__ T zero() { return 0; }
   static __device__ __forceinline__ T miss(T v, int32_t d) {
@@ -227,9 +358,9 @@ struct Piece<2> {
 // = v[src_of(r)]. Thread `t` of `nthreads` takes pieces t, t + nthreads, ..., with kInFlight
 // independent loads issued before the first store. An index outside [0, T) is filled like a
 // miss, so no index can make the kernel read outside v.
-template <int VEC, int kInFlight, int kInFlightP2, typename SrcFn>
-__device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, int64_t c0,
-                                            int nrows, int t, int nthreads, SrcFn src_of) {
+template <int VEC, int kInFlight, int kInFlightP2, bool NT, typename SrcFn>
+__device__ __forceinline__ void gather_rows_as(const GatherArgs& g, int64_t row, int64_t c0,
+                                               int nrows, int t, int nthreads, SrcFn src_of) {
   typedef Piece<VEC> P;
   const int64_t b = row / g.H, h = row - (row / g.H) * g.H;
   const uint8_t* vbase = g.v + b * g.v_sb + h * g.v_sh;
@@ -262,7 +393,7 @@ __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, in
         if (sv[u] == -2) continue;
         const typename P::T out = sv[u] >= 0 ? val[u]
                                   : (g.miss == LEMA_MISS_ZERO ? P::zero() : P::miss(val[u], g.dtype));
-        P::store(yp + static_cast<int64_t>(rb + u * rpp) * g.y_st, out);
+        P::template store<NT>(yp + static_cast<int64_t>(rb + u * rpp) * g.y_st, out);
       }
     }
     return;
@@ -298,9 +429,19 @@ __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, in
       if (kind[u] == 0) continue;
       const typename P::T out =
           kind[u] == 1 ? val[u] : (kind[u] == 2 ? P::miss(val[u], g.dtype) : P::zero());
-      P::store(to[u], out);
+      P::template store<NT>(to[u], out);
     }
   }
+}
+
+// The store kind is chosen once, outside the copy loops.
+template <int VEC, int kInFlight, int kInFlightP2, typename SrcFn>
+__device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, int64_t c0,
+                                            int nrows, int t, int nthreads, SrcFn src_of) {
+  if (g.nt)
+    gather_rows_as<VEC, kInFlight, kInFlightP2, true>(g, row, c0, nrows, t, nthreads, src_of);
+  else
+    gather_rows_as<VEC, kInFlight, kInFlightP2, false>(g, row, c0, nrows, t, nthreads, src_of);
 }
 
 // Find 4 keys at once (first bucket reads issued together); -1 where absent or inactive.
@@ -318,11 +459,27 @@ __device__ __forceinline__ void find4(const KeyT* base, const KeyT (&key)[4], Ke
   for (int i = 0; i < 4; ++i) slot[i] = table_find<KeyT, NB>(base, key[i], empty, b[i], x[i]);
 }
 
+// find4 for the keys with pass[i] set (the others get -1 without touching the table).
+template <typename KeyT, int NB>
+__device__ __forceinline__ void find4_masked(const KeyT* base, const KeyT (&key)[4], KeyT empty,
+                                             const bool (&pass)[4], int (&slot)[4]) {
+  int b[4];
+  KeyT x[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    b[i] = bucket_of<NB>(fold(key[i]));
+    if (pass[i]) read_bucket(base, b[i], x[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    slot[i] = pass[i] ? table_find<KeyT, NB>(base, key[i], empty, b[i], x[i]) : -1;
+}
+
 // Resolve the 1024 queries of chunk `chunk` of row `row` with the 256 threads t = 0..255
 // (four wavefronts), synchronising them with `bar`; leaves each thread's answers in src[p]
 // for positions p * 256 + t, and stores them to a.src when that is given. Every phase issues
 // the LDS reads (or CASes) of a thread's four positions together before waiting on any.
-template <typename CodeT, typename Bar>
+template <typename CodeT, typename Bar, bool kSumm = false>
 __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const ResolveArgs& a,
                                               int64_t row, int chunk, int t, Bar bar,
                                               int32_t (&src)[kPer]) {
@@ -343,27 +500,32 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
     kk[p] = act[p] ? krow[c0 + o] : CodeT(0);
   }
   // Keys before the chunk stream in batches of 1024 (4 per thread), latest batch first, the
-  // next batch loaded while the current one is looked up; c0 is a multiple of the batch.
+  // next kPrefetch batches loaded while the current one is looked up; c0 is a multiple of the
+  // batch.
   constexpr int kBatch = 4 * kThreads;
-  CodeT nxt[4];
-  auto load_batch = [&](int32_t j0) {
+  CodeT nxt[kPrefetch][4];
+  auto load_batch = [&](CodeT (&dst)[4], int32_t j0) {
     if (a.kvec) {  // 4 consecutive codes per thread, 16-byte aligned
       const CodeT* p = krow + j0 + 4 * t;
       if constexpr (sizeof(CodeT) == 4) {
         const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-        nxt[0] = v.x; nxt[1] = v.y; nxt[2] = v.z; nxt[3] = v.w;
+        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
       } else {
         const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
         const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 2);
-        nxt[0] = (uint64_t(v0.y) << 32) | v0.x; nxt[1] = (uint64_t(v0.w) << 32) | v0.z;
-        nxt[2] = (uint64_t(v1.y) << 32) | v1.x; nxt[3] = (uint64_t(v1.w) << 32) | v1.z;
+        dst[0] = (uint64_t(v0.y) << 32) | v0.x; dst[1] = (uint64_t(v0.w) << 32) | v0.z;
+        dst[2] = (uint64_t(v1.y) << 32) | v1.x; dst[3] = (uint64_t(v1.w) << 32) | v1.z;
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) nxt[e] = krow[j0 + e * kThreads + t];
+      for (int e = 0; e < 4; ++e) dst[e] = krow[j0 + e * kThreads + t];
     }
   };
-  if (c0 > 0) load_batch(c0 - kBatch);
+  if constexpr (!kSumm) {
+#pragma unroll
+    for (int d = 0; d < kPrefetch; ++d)
+      if (c0 - (d + 1) * kBatch >= 0) load_batch(nxt[d], c0 - (d + 1) * kBatch);
+  }
 
   for (int x = t; x < kSlots; x += kThreads) s.code[x] = SENT;
   for (int x = t; x <= kSlots; x += kThreads) {
@@ -374,7 +536,12 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
     s.mkey[x] = kMapEmpty;
     s.mbits[x] = 0;
   }
-  if (t == 0) s.sent_used = 0;
+  for (int x = t; x < kFilterWords; x += kThreads) s.qbits[x] = 0;
+  if (t == 0) {
+    s.sent_used = 0;
+    s.nq = 0;
+    s.nneed = 0;
+  }
   bar();
 
   // 1. the chunk's query codes -> table slots; the sentinel code has its own slot kSlots
@@ -384,121 +551,184 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
 #pragma unroll
   for (int p = 0; p < kPer; ++p) {
     qs[p] = kSlots;
-    if (!act[p]) continue;
-    if (q[p] == SENT) {
-      s.sent_used = 1;
-      continue;
+    bool ins = false;
+    if (act[p]) {
+      if (q[p] == SENT)
+        s.sent_used = 1;
+      else
+        qs[p] = table_claim<CodeT, kBuckets>(s.code, q[p], SENT, bucket_of<kBuckets>(fold(q[p])), ins);
     }
-    bool ins;
-    qs[p] = table_claim<CodeT, kBuckets>(s.code, q[p], SENT, bucket_of<kBuckets>(fold(q[p])), ins);
-  }
-  bar();
-
-  const bool sent_used = s.sent_used != 0;
-  // slots among the query codes of 4 key codes (-1 = no query of the chunk asks for it)
-  auto find_codes = [&](const CodeT (&c)[4], int (&sl)[4]) {
-    find4<CodeT, kBuckets>(s.code, c, SENT, sl);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (c[i] == SENT) sl[i] = sent_used ? kSlots : -1;
-  };
-
-  // 2a. keys inside the chunk: each sets its lane in its (code, word) mask; the key that
-  // creates a (code, word) entry also sets the word's bit in the code's summary
-  {
-    int sl[kPer];
-    find_codes(kk, sl);
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      if (!act[p] || sl[p] < 0) continue;
-      const int wd = (p * kThreads + t) >> 6;
-      const uint32_t key = (static_cast<uint32_t>(sl[p]) << 4) | wd;
-      bool ins;
-      const int m = table_claim<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty,
-                                                       bucket_of<kMapBuckets>(key), ins);
-      atomicOr(reinterpret_cast<unsigned long long*>(&s.mbits[m]), 1ull << lane);
-      if (ins)
-        atomicOr(reinterpret_cast<uint32_t*>(&s.summ[sl[p] & ~1]), (1u << wd) << (16 * (sl[p] & 1)));
-    }
-  }
-  // 2b. keys before the chunk raise their code's latest position. Walking backwards, a code
-  // whose latest position is already known skips the atomic, so only the first batch that
-  // holds a popular code contends on its slot.
-  for (int32_t j0 = c0 - kBatch; j0 >= 0; j0 -= kBatch) {
-    CodeT cur[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) cur[e] = nxt[e];
-    if (j0 > 0) load_batch(j0 - kBatch);
-    int sl[4];
-    find_codes(cur, sl);
-    int32_t known[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) known[e] = s.pos[sl[e] >= 0 ? sl[e] : kSlots];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int32_t j = a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
-      if (sl[e] >= 0 && known[e] < j) atomicMax(&s.pos[sl[e]], j);
+    if (LEMA_RESOLVE_FILTER == 2) {  // every lane of the wavefront takes part in the count
+      const int n = __popcll(__ballot(ins));
+      if (lane == 0 && n) atomicAdd(&s.nq, n);
     }
   }
   bar();
-
-  // 3. resolve: the latest earlier lane of the own word, else the latest earlier word of the
-  // chunk holding the code, else the latest position before the chunk
-  {
-    int m[kPer];
-    uint32_t key[kPer];
+  // the filter, when the chunk's query codes are many (few keys then carry one)
+  const bool filt = LEMA_RESOLVE_FILTER == 1 || (LEMA_RESOLVE_FILTER == 2 && s.nq > kFilterMinCodes);
+  // The rest is compiled twice, with and without the filter, so that chunks without it run
+  // the code they ran before it existed.
+  auto rest = [&](auto filter_on) {
+    constexpr bool kFilt = decltype(filter_on)::value;
+    if constexpr (kFilt) {
 #pragma unroll
-    for (int p = 0; p < kPer; ++p)
-      key[p] = (static_cast<uint32_t>(qs[p]) << 4) | ((p * kThreads + t) >> 6);
-    find4<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty, m);
-    uint64_t bits[kPer];
-    uint32_t words[kPer];
-    int32_t before[kPer];
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {  // every read a position may need, issued together
-      bits[p] = s.mbits[m[p] >= 0 ? m[p] : 0];
-      words[p] = s.summ[qs[p]];
-      before[p] = s.pos[qs[p]];
+      for (int p = 0; p < kPer; ++p) {
+        if (!act[p] || q[p] == SENT) continue;
+        const uint32_t h = filter_hash(fold(q[p]));
+        atomicOr(&s.qbits[h >> 5], 1u << (h & 31));
+      }
+      bar();
     }
-    uint32_t key2[kPer];
-    bool second[kPer];
+
+    const bool sent_used = s.sent_used != 0;
+    // slots among the query codes of 4 key codes (-1 = no query of the chunk asks for it)
+    auto find_codes = [&](const CodeT (&c)[4], int (&sl)[4]) {
+      if constexpr (kFilt) {
+        bool pass[4];
 #pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int wd = (p * kThreads + t) >> 6;
-      const uint64_t below = m[p] >= 0 ? (bits[p] & ((1ull << lane) - 1)) : 0;
-      const uint32_t w_below = words[p] & ((1u << wd) - 1);
-      second[p] = false;
-      key2[p] = kMapEmpty;
-      if (!act[p]) {
-        src[p] = -1;
-      } else if (below) {
-        src[p] = c0 + (wd << 6) + 63 - __clzll(below);
-      } else if (w_below) {
-        const int w2 = 31 - __clz(w_below);
-        second[p] = true;
-        key2[p] = (static_cast<uint32_t>(qs[p]) << 4) | w2;
-        src[p] = c0 + (w2 << 6);
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t h = filter_hash(fold(c[i]));
+          pass[i] = (s.qbits[h >> 5] >> (h & 31)) & 1u;
+        }
+        find4_masked<CodeT, kBuckets>(s.code, c, SENT, pass, sl);
       } else {
-        src[p] = before[p];
+        find4<CodeT, kBuckets>(s.code, c, SENT, sl);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (c[i] == SENT) sl[i] = sent_used ? kSlots : -1;
+    };
+
+    // 2a. keys inside the chunk: each sets its lane in its (code, word) mask; the key that
+    // creates a (code, word) entry also sets the word's bit in the code's summary
+    {
+      int sl[kPer];
+      find_codes(kk, sl);
+#pragma unroll
+      for (int p = 0; p < kPer; ++p) {
+        if (!act[p] || sl[p] < 0) continue;
+        const int wd = (p * kThreads + t) >> 6;
+        const uint32_t key = (static_cast<uint32_t>(sl[p]) << 4) | wd;
+        bool ins;
+        const int m = table_claim<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty,
+                                                         bucket_of<kMapBuckets>(key), ins);
+        atomicOr(reinterpret_cast<unsigned long long*>(&s.mbits[m]), 1ull << lane);
+        if (ins)
+          atomicOr(reinterpret_cast<uint32_t*>(&s.summ[sl[p] & ~1]), (1u << wd) << (16 * (sl[p] & 1)));
       }
     }
-    int m2[kPer];
-    find4<uint32_t, kMapBuckets>(s.mkey, key2, kMapEmpty, m2);
+    // 2b. keys before the chunk raise their code's latest position. Walking backwards, a code
+    // whose latest position is already known skips the atomic, so only the first batch that
+    // holds a popular code contends on its slot.
+    for (int32_t jb = kSumm ? -1 : c0 - kBatch; jb >= 0; jb -= kPrefetch * kBatch) {
 #pragma unroll
-    for (int p = 0; p < kPer; ++p)
-      if (second[p]) src[p] += 63 - __clzll(s.mbits[m2[p]]);
-  }
-  if (a.src != nullptr) {
+      for (int d = 0; d < kPrefetch; ++d) {
+        const int32_t j0 = jb - d * kBatch;
+        if (j0 < 0) break;
+        CodeT cur[4];
 #pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int o = p * kThreads + t;
-      if (o >= n_here) continue;
-      if (a.src_bytes == 8)
-        static_cast<int64_t*>(a.src)[row * a.T + c0 + o] = src[p];
-      else
-        static_cast<int32_t*>(a.src)[row * a.T + c0 + o] = src[p];
+        for (int e = 0; e < 4; ++e) cur[e] = nxt[d][e];
+        if (j0 - kPrefetch * kBatch >= 0) load_batch(nxt[d], j0 - kPrefetch * kBatch);
+        int sl[4];
+        find_codes(cur, sl);
+        int32_t known[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) known[e] = s.pos[sl[e] >= 0 ? sl[e] : kSlots];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t j = a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
+          if (sl[e] >= 0 && known[e] < j) atomicMax(&s.pos[sl[e]], j);
+        }
+      }
     }
-  }
+    bar();
+
+    // 3. resolve: the latest earlier lane of the own word, else the latest earlier word of the
+    // chunk holding the code, else the latest position before the chunk
+    bool nb[kPer];  // the answer is the code's latest position before the chunk
+    {
+      int m[kPer];
+      uint32_t key[kPer];
+#pragma unroll
+      for (int p = 0; p < kPer; ++p)
+        key[p] = (static_cast<uint32_t>(qs[p]) << 4) | ((p * kThreads + t) >> 6);
+      find4<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty, m);
+      uint64_t bits[kPer];
+      uint32_t words[kPer];
+      int32_t before[kPer];
+#pragma unroll
+      for (int p = 0; p < kPer; ++p) {  // every read a position may need, issued together
+        bits[p] = s.mbits[m[p] >= 0 ? m[p] : 0];
+        words[p] = s.summ[qs[p]];
+        before[p] = s.pos[qs[p]];
+      }
+      uint32_t key2[kPer];
+      bool second[kPer];
+#pragma unroll
+      for (int p = 0; p < kPer; ++p) {
+        const int wd = (p * kThreads + t) >> 6;
+        const uint64_t below = m[p] >= 0 ? (bits[p] & ((1ull << lane) - 1)) : 0;
+        const uint32_t w_below = words[p] & ((1u << wd) - 1);
+        second[p] = false;
+        nb[p] = false;
+        key2[p] = kMapEmpty;
+        if (!act[p]) {
+          src[p] = -1;
+        } else if (below) {
+          src[p] = c0 + (wd << 6) + 63 - __clzll(below);
+        } else if (w_below) {
+          const int w2 = 31 - __clz(w_below);
+          second[p] = true;
+          key2[p] = (static_cast<uint32_t>(qs[p]) << 4) | w2;
+          src[p] = c0 + (w2 << 6);
+        } else {
+          src[p] = before[p];
+          nb[p] = true;
+        }
+      }
+      int m2[kPer];
+      find4<uint32_t, kMapBuckets>(s.mkey, key2, kMapEmpty, m2);
+#pragma unroll
+      for (int p = 0; p < kPer; ++p)
+        if (second[p]) src[p] += 63 - __clzll(s.mbits[m2[p]]);
+    }
+    if (kSumm && chunk > 0) {
+      // Summary path: the codes some query needs from before the chunk are listed (in the key
+      // map's storage, dead by now) and each is looked up in the earlier chunks' summaries.
+#pragma unroll
+      for (int p = 0; p < kPer; ++p)
+        if (nb[p]) s.pos[qs[p]] = -2;
+      bar();
+      int32_t* need = reinterpret_cast<int32_t*>(s.mkey);
+      for (int x = t; x <= kSlots; x += kThreads)
+        if (s.pos[x] == -2) need[atomicAdd(&s.nneed, 1)] = x;
+      bar();
+      const int nneed = s.nneed;
+      for (int i = t; i < nneed; i += kThreads) {
+        const int x = need[i];
+        s.pos[x] = before_chunk<CodeT>(a, row, chunk, x == kSlots ? SENT : s.code[x], x == kSlots);
+      }
+      bar();
+#pragma unroll
+      for (int p = 0; p < kPer; ++p)
+        if (nb[p]) src[p] = s.pos[qs[p]];
+    }
+    if (a.src != nullptr) {
+#pragma unroll
+      for (int p = 0; p < kPer; ++p) {
+        const int o = p * kThreads + t;
+        if (o >= n_here) continue;
+        if (a.src_bytes == 8)
+          static_cast<int64_t*>(a.src)[row * a.T + c0 + o] = src[p];
+        else
+          static_cast<int32_t*>(a.src)[row * a.T + c0 + o] = src[p];
+      }
+    }
+  };
+  if (filt)
+    rest(std::true_type{});
+  else
+    rest(std::false_type{});
 }
 
 }  // namespace

@@ -274,3 +274,211 @@ def test_runs_on_current_stream(dev):
     s.synchronize()
     want = oracle.latest_prev_match(qc.reshape(8, -1), kc.reshape(8, -1))
     assert np.array_equal(src.cpu().numpy().reshape(8, -1), want)
+
+
+# --------------------------------------------------- chunk-summary path (workspace entries)
+def resolve_c(qc: torch.Tensor, kc: torch.Tensor, ws: bool) -> np.ndarray:
+    """latest_prev_match through the C ABI: the backward scan (no workspace) or the chunk
+    summaries (lema_latest_prev_match_ws)."""
+    from latest_exact_match_attention_amd import _lib
+    N, T = qc.shape
+    src = torch.empty((N, T), dtype=torch.int64, device=qc.device)
+    L, st = _lib.lib(), _lib.stream_of(qc)
+    if ws:
+        n = L.lema_resolve_workspace_bytes(N, T)
+        w = torch.empty(max(n, 1), dtype=torch.uint8, device=qc.device)
+        _lib.check(L.lema_latest_prev_match_ws(qc.data_ptr(), kc.data_ptr(), qc.element_size(), N,
+                                               T, src.data_ptr(), 8, w.data_ptr() if n else None,
+                                               n, st))
+    else:
+        _lib.check(L.lema_latest_prev_match(qc.data_ptr(), kc.data_ptr(), qc.element_size(), N, T,
+                                            src.data_ptr(), 8, st))
+    return src.cpu().numpy()
+
+
+def both_paths(qc: np.ndarray, kc: np.ndarray, dev, code_dtype) -> np.ndarray:
+    q = torch.from_numpy(qc).to(dev).to(code_dtype)
+    k = torch.from_numpy(kc).to(dev).to(code_dtype)
+    want = oracle.latest_prev_match(qc, kc)
+    assert np.array_equal(resolve_c(q, k, ws=False), want)
+    assert np.array_equal(resolve_c(q, k, ws=True), want)
+    return want
+
+
+LONG = 64 * 1024 + 464          # rows of 65 chunks (ragged last chunk) take the summaries
+
+
+@pytest.mark.parametrize("T", [64 * 1024 - 1024, 64 * 1024 - 1023, LONG])
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_summary_path_equals_scan(dev, T, code_dtype):
+    """Rows at the summaries' threshold (64 chunks) and past it, ragged last chunk included:
+    both paths equal the oracle, on few-code rows (matches within a chunk), many-code rows
+    (matches across chunks) and far copies (matches many chunks back)."""
+    from latest_exact_match_attention_amd import _lib
+    assert (_lib.lib().lema_resolve_workspace_bytes(4, T) > 0) == (T > 63 * 1024)
+    rng = np.random.default_rng(T)
+    rows = [rng.integers(0, 7, T), rng.integers(0, 30000, T), rng.integers(-2, 2, T)]
+    far = rng.integers(0, 1 << 31, T)
+    far[T // 2:] = far[:T - T // 2]          # every key of the second half repeats one
+    rows.append(far)
+    kc = np.stack(rows)
+    i = np.arange(T)
+    # row 3: query i >= T/2 asks for the key of i - T/2 (its copy at i itself is not < i)
+    q3 = np.where(i >= T // 2, far[np.maximum(i - T // 2, 0)], rng.integers(0, 1 << 31, T))
+    qc = np.stack([rng.integers(0, 7, T), rng.integers(0, 30000, T), rng.integers(-2, 2, T), q3])
+    want = both_paths(qc, kc, dev, code_dtype)
+    assert (want[3] >= 0).mean() > 0.4
+
+
+def test_summary_fold_collisions(dev):
+    """64-bit codes x and x ^ (m << 32 | m) fold to the same 32 bits, so they share the
+    summary bucket and fingerprint: only the check against the key code tells them apart."""
+    T, m, late = LONG, 0x5A5A5A5A, 40 * 1024
+    rng = np.random.default_rng(3)
+    base = rng.integers(1, 1 << 62, 40)
+    twin = base ^ ((m << 32) | m)
+    pool = np.concatenate([base, twin])
+    kc = pool[rng.integers(0, 80, (3, T))]
+    qc = pool[rng.integers(0, 80, (3, T))]
+    kc[2, late:] = twin[0]                    # row 2: late keys are all the twin of base[0]
+    qc[2, late:] = base[0]                    # so base[0] is found before chunk 40 only
+    want = both_paths(qc, kc, dev, torch.int64)
+    assert (want[2, late + 1:] < late).all() and (want[2, late + 1:] >= 0).all()
+
+
+def _fib_bucket(x):
+    return ((x * 0x9E3779B1) & 0xFFFFFFFF) * 512 >> 32
+
+
+def _fingerprint(h):
+    h = h ^ (h >> 16)
+    h = (h * 0x85EBCA6B) & 0xFFFFFFFF
+    h ^= h >> 13
+    h = (h * 0xC2B2AE35) & 0xFFFFFFFF
+    h ^= h >> 16
+    f = h >> 10
+    return np.where(f == 0x3FFFFF, 0x3FFFFE, f)
+
+
+def test_summary_fingerprint_collisions(dev):
+    """32-bit codes with the same summary bucket and fingerprint (found by brute force): a
+    chunk holding one of them must not answer for the other."""
+    rng = np.random.default_rng(5)
+    x = np.unique(rng.integers(0, 1 << 32, 1 << 21, dtype=np.uint64))
+    key = (_fib_bucket(x) << 22) | _fingerprint(x)
+    order = np.argsort(key, kind="stable")
+    ks = key[order]
+    dup = np.nonzero(ks[1:] == ks[:-1])[0]
+    pairs = [(int(x[order[i]]), int(x[order[i + 1]])) for i in dup]
+    pairs = [(a, b) for a, b in pairs if min(a, b) >= 1 << 20][:6]   # apart from the filler
+    assert len(pairs) == 6
+    T = LONG
+    kc = np.zeros((len(pairs), T), dtype=np.int64)
+    qc = np.zeros((len(pairs), T), dtype=np.int64)
+    for r, (a, b) in enumerate(pairs):
+        kc[r] = rng.integers(0, 1 << 20, T)
+        kc[r, 100] = a                         # a early (chunk 0), b in every later chunk
+        kc[r, 1024::512] = b
+        qc[r] = rng.integers(0, 1 << 20, T)
+        qc[r, 2048::7] = a
+    want = both_paths(qc.astype(np.uint32).view(np.int32).astype(np.int64),
+                      kc.astype(np.uint32).view(np.int32).astype(np.int64), dev, torch.int32)
+    assert (want[:, 2048::7] == 100).all()
+
+
+def test_summary_full_buckets(dev):
+    """Chunks of 1024 distinct uniform 32-bit keys (summary tables at load 1/2, so some
+    buckets are full and probes continue), queries copying keys from any earlier chunk."""
+    rng = np.random.default_rng(9)
+    T = LONG
+    kc = rng.integers(0, 1 << 32, (3, T), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    back = rng.integers(1, T, (3, T))
+    i = np.arange(T)
+    qc = np.where(i - back >= 0, np.take_along_axis(kc, np.maximum(i - back, 0), 1), 12345)
+    qc = qc.astype(np.int32)
+    want = both_paths(qc.astype(np.int64), kc.astype(np.int64), dev, torch.int32)
+    assert (want >= 0).mean() > 0.45
+
+
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_summary_all_ones_code(dev, code_dtype):
+    """The all-ones code is the summary tables' empty marker and is kept apart; as a code it
+    is found across chunks like any other."""
+    T = LONG
+    rng = np.random.default_rng(2)
+    kc = rng.choice([-1, 0, 1, 9], size=(3, T))
+    qc = rng.choice([-1, 0, 1, 7], size=(3, T))
+    kc[1] = 5
+    kc[1, 1500] = -1                           # the only all-ones key of row 1, in chunk 1
+    qc[1] = -1
+    kc[2] = 5
+    kc[2, 65000] = -1
+    qc[2, :] = -1
+    want = both_paths(qc, kc, dev, code_dtype)
+    assert (want[1, 1501:] == 1500).all()
+    assert (want[2, 65001:] == 65000).all() and (want[2, :65001] == -1).all()
+
+
+def test_hard_ws_equals_hard(dev):
+    """lema_hard_ws (summaries + fused gather) writes the same y and src bytes as lema_hard."""
+    from latest_exact_match_attention_amd import _lib
+    from latest_exact_match_attention_amd.attention import resolve_workspace
+    B, H, T, dv = 1, 3, LONG, 24
+    rng = np.random.default_rng(4)
+    qc = torch.from_numpy(rng.integers(0, 900, (B * H, T))).to(dev).to(torch.int32)
+    kc = torch.from_numpy(rng.integers(0, 900, (B * H, T))).to(dev).to(torch.int32)
+    v = torch.randn(B, H, T, dv, device=dev, dtype=torch.bfloat16)
+    outs = []
+    for ws in (None, resolve_workspace(B * H, T, dev)):
+        y = torch.empty_like(v)
+        src = torch.empty((B, H, T), dtype=torch.int32, device=dev)
+        args = [qc.data_ptr(), kc.data_ptr(), 4, v.data_ptr(), _lib.DTYPE_CODE[v.dtype], B, H, T,
+                dv, *v.stride()[:3], y.data_ptr(), *y.stride()[:3], _lib.MISS_DENSE,
+                src.data_ptr(), 4]
+        if ws is None:
+            _lib.check(_lib.lib().lema_hard(*args, _lib.stream_of(v)))
+        else:
+            _lib.check(_lib.lib().lema_hard_ws(*args, ws.data_ptr(), ws.numel(),
+                                               _lib.stream_of(v)))
+        outs.append((y, src))
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    want = oracle.latest_prev_match(qc.cpu().numpy(), kc.cpu().numpy())
+    assert np.array_equal(outs[1][1].cpu().numpy().reshape(B * H, T), want)
+
+
+def test_summary_workspace_too_small(dev):
+    from latest_exact_match_attention_amd import _lib
+    N, T = 2, LONG
+    q = torch.zeros((N, T), dtype=torch.int32, device=dev)
+    src = torch.empty((N, T), dtype=torch.int64, device=dev)
+    n = _lib.lib().lema_resolve_workspace_bytes(N, T)
+    w = torch.empty(n, dtype=torch.uint8, device=dev)
+    rc = _lib.lib().lema_latest_prev_match_ws(q.data_ptr(), q.data_ptr(), 4, N, T, src.data_ptr(),
+                                              8, w.data_ptr(), n - 256, _lib.stream_of(q))
+    assert rc != 0 and b"workspace" in _lib.lib().lema_last_error()
+
+
+@pytest.mark.parametrize("T", [2500, 4096])
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("alphabet", [1 << 24, 40])
+def test_grouped_rows_interleaved_y(dev, T, code_dtype, alphabet):
+    """64 heads (rows in whole groups of 64: the grouped workgroup order) with v and y viewed
+    from [B, T, H * dv] like the projections (y rows interleaved: plain stores merged in L2),
+    codes that seldom repeat (the key filter on) or often (off): y and src bit-exact."""
+    B, H, dv = 2, 64, 24
+    rng = np.random.default_rng(T + alphabet)
+    qc = rng.integers(0, alphabet, (B * H, T))
+    kc = rng.integers(0, alphabet, (B * H, T))
+    qc[:, T // 2::5] = kc[:, T // 3: T // 3 + len(range(T // 2, T, 5))]   # some far matches
+    vp = torch.randn(B, T, H * dv, device=dev).to(torch.bfloat16)
+    v = vp.view(B, T, H, dv).transpose(1, 2)
+    y, src = lema_from_codes(torch.from_numpy(qc).to(dev).to(code_dtype).view(B, H, T),
+                             torch.from_numpy(kc).to(dev).to(code_dtype).view(B, H, T), v,
+                             return_src=True)
+    want_src = oracle.latest_prev_match(qc, kc)
+    assert np.array_equal(src.cpu().numpy().reshape(B * H, T), want_src)
+    vb = bits16(v).reshape(B * H, T, dv)
+    want_y = oracle.gather(vb, "bf16", want_src, 0)
+    assert same_values(bits16(y).reshape(B * H, T, dv), want_y, "bf16")
+    assert (want_src >= 0).any()
