@@ -461,21 +461,48 @@ __device__ __forceinline__ int64_t gt_home(uint64_t key, int64_t cap) {
   return static_cast<int64_t>(splitmix_fin(key) & static_cast<uint64_t>(cap - 1));
 }
 
-// Find or enter `key` in the group table (one thread); the table is at most half full.
-__device__ __forceinline__ int64_t gt_claim(const BulkWs& w, uint64_t key) {
-  int64_t sl = gt_home(key, w.gt_cap);
-  for (int64_t left = w.gt_cap; left > 0; --left) {
-    const uint64_t k = w.gt[sl].key;
-    if (k == key) return sl;
-    if (k == 0) {
-      const unsigned long long old =
-          atomicCAS(reinterpret_cast<unsigned long long*>(&w.gt[sl].key), 0ull,
-                    static_cast<unsigned long long>(key));
-      if (old == 0 || old == key) return sl;
-    }
-    sl = (sl + 1) & (w.gt_cap - 1);
+// Find or enter U keys in the group table (one thread; the table is at most half full): the
+// slots, -1 for an inactive key or one that found no room. The keys' probes advance together,
+// so each round's reads, then its CASes, are in flight at once.
+template <int U>
+__device__ __forceinline__ void gt_claim(const BulkWs& w, const uint64_t (&key)[U],
+                                         const bool (&act)[U], int64_t (&g)[U]) {
+  int64_t sl[U], left[U];
+  bool todo[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    sl[u] = gt_home(key[u], w.gt_cap);
+    left[u] = w.gt_cap;
+    todo[u] = act[u];
+    g[u] = -1;
   }
-  return -1;
+  for (;;) {
+    bool any = false;
+    uint64_t k[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) k[u] = todo[u] ? w.gt[sl[u]].key : 0ull;
+    unsigned long long old[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      old[u] = 1ull;  // not a claim
+      if (todo[u] && k[u] == 0)
+        old[u] = atomicCAS(reinterpret_cast<unsigned long long*>(&w.gt[sl[u]].key), 0ull,
+                           static_cast<unsigned long long>(key[u]));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!todo[u]) continue;
+      if (k[u] == key[u] || (k[u] == 0 && (old[u] == 0 || old[u] == key[u]))) {
+        g[u] = sl[u];  // found, claimed, or claimed by a twin of this key first
+        todo[u] = false;
+      } else {         // the slot holds another key (seen, or won by it first): the next
+        sl[u] = (sl[u] + 1) & (w.gt_cap - 1);
+        if (--left[u] == 0) todo[u] = false;
+      }
+      any = any || todo[u];
+    }
+    if (!any) return;
+  }
 }
 
 // Slot of `key` in the group table or -1, kGroup lanes probing kGroup slots per read.
@@ -572,20 +599,34 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
   uint32_t* scode = w.sum_code + sum * kSlots;
   int32_t* spos = w.sum_pos + sum * kSumPos;
   for (int x = t; x < kSlots; x += kThreads) scode[x] = s.code[x];
-  for (int x = t; x <= kSlots; x += kThreads) {
-    const int32_t lp = s.pos[x];
-    spos[x] = lp;
-    if (lp < 0) continue;
-    const uint32_t code = x < kSlots ? s.code[x] : SENT;
-    const uint64_t key = (static_cast<uint64_t>(p + 1) << 32) | code;
-    const int64_t g = gt_claim(w, key);
-    if (g < 0) {  // cannot happen with the table at most half full; fail loudly
-      atomicOr(a.full, 2);
-      continue;
+  for (int x = t; x <= kSlots; x += kThreads) spos[x] = s.pos[x];
+  constexpr int U = 4;  // codes per thread whose claims overlap
+  for (int x0 = t; x0 <= kSlots; x0 += U * kThreads) {
+    int32_t lp[U];
+    uint32_t code[U];
+    uint64_t key[U];
+    bool act[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int x = x0 + u * kThreads;
+      lp[u] = x <= kSlots ? s.pos[x] : -1;
+      code[u] = x < kSlots ? s.code[x] : SENT;
+      key[u] = (static_cast<uint64_t>(p + 1) << 32) | code[u];
+      act[u] = lp[u] >= 0;
     }
-    atomicOr(reinterpret_cast<unsigned long long*>(&w.gt[g].mask), 1ull << c);
-    atomicMax(&w.gt[g].last, c * kChunk + lp);
-    if (code == 0) w.zero_slot[p] = g;
+    int64_t g[U];
+    gt_claim<U>(w, key, act, g);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!act[u]) continue;
+      if (g[u] < 0) {  // cannot happen with the table at most half full; fail loudly
+        atomicOr(a.full, 2);
+        continue;
+      }
+      atomicOr(reinterpret_cast<unsigned long long*>(&w.gt[g[u]].mask), 1ull << c);
+      atomicMax(&w.gt[g[u]].last, c * kChunk + lp[u]);
+      if (code[u] == 0) w.zero_slot[p] = g[u];
+    }
   }
 }
 
