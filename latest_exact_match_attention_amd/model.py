@@ -214,7 +214,8 @@ class SwiGLU(nn.Module):
     def forward(self, x, residual=None):
         """down(silu(gate(x)) * up(x)), plus `residual` when given (Block's x + mlp(h)). On
         decode shapes the gate, up and product are one launch and the down projection adds
-        the residual in its epilogue."""
+        the residual in its epilogue; on longer bf16 inputs without autograd the down GEMM
+        accumulates into `residual` itself, which is then returned."""
         g, u, dn = self.gate.weight, self.up.weight, self.down.weight
         if _skinny(x, g) and g.shape == u.shape and u.data_ptr() % 16 == 0 and u.is_contiguous():
             K, N = x.shape[-1], g.shape[0]
@@ -233,6 +234,15 @@ class SwiGLU(nn.Module):
                 return y
         else:
             a = swiglu(linear(x, self.gate), linear(x, self.up))
+            if residual is not None and not _skinny(a, dn) and a.is_cuda and \
+                    a.dtype == residual.dtype == dn.dtype == torch.bfloat16 and \
+                    residual.is_contiguous() and not torch.is_grad_enabled():
+                # the residual add in the GEMM's epilogue, accumulating into `residual` in
+                # place (one rounding of x + a . W^T where the two torch ops round twice;
+                # within the forward's tolerance), 2-D operands
+                D = dn.shape[0]
+                residual.view(-1, D).addmm_(a.reshape(-1, a.shape[-1]), dn.t())
+                return residual
         y = linear(a, self.down)
         return y if residual is None else residual + y
 
