@@ -631,9 +631,9 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         if (j0 - kPrefetch * kBatch >= 0) load_batch(nxt[d], j0 - kPrefetch * kBatch);
         int sl[4];
         find_codes(cur, sl);
-        int32_t known[4];
+        int32_t known[4];  // read only for keys of query codes (the others raise nothing)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) known[e] = s.pos[sl[e] >= 0 ? sl[e] : kSlots];
+        for (int e = 0; e < 4; ++e) known[e] = sl[e] >= 0 ? s.pos[sl[e]] : 0x7FFFFFFF;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int32_t j = a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
