@@ -7,7 +7,8 @@
 // aligned): a wavefront takes 64 consecutive rows in MEMORY order, i.e. 64*D consecutive
 // elements; each lane turns 8 consecutive elements (one 16-byte load) into one byte of the
 // rows' concatenated bit string in LDS, and lane l then cuts its row's D bits out of it and
-// writes the code to its (b, h, t) slot.
+// writes the code to its (b, h, t) slot -- or, when 64 heads are innermost in memory and the
+// codes run along positions, a workgroup stages 32 positions x 64 heads and writes runs.
 // Generic path (any strides, last dim contiguous): one thread per row.
 #include "lema_internal.h"
 
@@ -89,14 +90,11 @@ __device__ __forceinline__ uint32_t sign_byte(const Raw8<DTYPE>& r) {
 // elements. Each lane reads 16 (32 for fp32) bytes per step -- 8 elements, their 8 sign bits
 // one byte of the rows' concatenated bit string, staged in LDS -- so the wavefront covers
 // the string in ceil(D / 8) coalesced steps; lane l then cuts row l's D bits out of it.
-template <int DTYPE, typename CodeT>
-__global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
-  __shared__ uint64_t words[kPackThreads / 64][64 + 1];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * (kPackThreads / 64) + w) * 64;
-  if (m0 >= a.R) return;
+template <int DTYPE>
+__device__ __forceinline__ uint64_t row_code(const DenseArgs& a, uint64_t* words, int64_t m0,
+                                             int lane) {
   const int64_t e0 = m0 * a.D, eend = a.R * a.D;
-  uint8_t* bytes = reinterpret_cast<uint8_t*>(words[w]);
+  uint8_t* bytes = reinterpret_cast<uint8_t*>(words);
   const int steps = (a.D + 7) / 8;  // 8 * D bytes of bit string, 64 bytes per step
   const bool whole = e0 + 64 * static_cast<int64_t>(a.D) <= eend;  // no array end inside
   if (whole) {
@@ -122,21 +120,61 @@ __global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
       bytes[b] = static_cast<uint8_t>(m);
     }
   }
-  if (lane == 0) words[w][a.D] = 0;
+  if (lane == 0) words[a.D] = 0;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int64_t m = m0 + lane;
-  if (m >= a.R) return;
   const int bitpos = lane * a.D;
   const int wi = bitpos >> 6, off = bitpos & 63;
-  uint64_t code = words[w][wi] >> off;
-  if (off != 0 && off + a.D > 64) code |= words[w][wi + 1] << (64 - off);
+  uint64_t code = words[wi] >> off;
+  if (off != 0 && off + a.D > 64) code |= words[wi + 1] << (64 - off);
   if (a.D < 64) code &= (uint64_t(1) << a.D) - 1;
+  __builtin_amdgcn_wave_barrier();  // the bit string is read before the next row group's
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return code;
+}
+
+__device__ __forceinline__ int64_t out_index(const DenseArgs& a, int64_t m) {
   const int64_t i2 = m % a.E2;
   const int64_t r = m / a.E2;
   const int64_t i1 = r % a.E1, i0 = r / a.E1;
-  static_cast<CodeT*>(a.codes)[i0 * a.os0 + i1 * a.os1 + i2 * a.os2] = static_cast<CodeT>(code);
+  return i0 * a.os0 + i1 * a.os1 + i2 * a.os2;
+}
+
+template <int DTYPE, typename CodeT>
+__global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
+  __shared__ uint64_t words[kPackThreads / 64][64 + 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * (kPackThreads / 64) + w) * 64;
+  if (m0 >= a.R) return;
+  const uint64_t code = row_code<DTYPE>(a, words[w], m0, lane);
+  const int64_t m = m0 + lane;
+  if (m >= a.R) return;
+  static_cast<CodeT*>(a.codes)[out_index(a, m)] = static_cast<CodeT>(code);
+}
+
+// Rows of 64 heads innermost in memory (the [B, T, H * D] projection viewed as [B, H, T, D])
+// whose codes go to [B, H, T]: a wavefront's 64 codes would land T apart. A workgroup packs
+// 32 consecutive row groups (positions) instead, 8 per wavefront, stages the [32][64] codes in
+// LDS and writes each head's 32 positions as one contiguous run.
+constexpr int kTileGroups = 32;
+template <int DTYPE, typename CodeT>
+__global__ __launch_bounds__(kPackThreads) void pack_tile_kernel(DenseArgs a) {
+  __shared__ uint64_t words[kPackThreads / 64][64 + 1];
+  __shared__ CodeT tile[kTileGroups][64 + 1];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTileGroups * 64;
+  for (int g = w; g < kTileGroups; g += kPackThreads / 64) {
+    const int64_t m0 = base + static_cast<int64_t>(g) * 64;
+    if (m0 < a.R) tile[g][lane] = static_cast<CodeT>(row_code<DTYPE>(a, words[w], m0, lane));
+  }
+  __syncthreads();
+  for (int idx = t; idx < kTileGroups * 64; idx += kPackThreads) {
+    const int h = idx / kTileGroups, g = idx % kTileGroups;  // consecutive threads: positions
+    const int64_t m = base + static_cast<int64_t>(g) * 64 + h;
+    if (m < a.R) static_cast<CodeT*>(a.codes)[out_index(a, m)] = tile[g][h];
+  }
 }
 
 struct StridedArgs {
@@ -163,6 +201,16 @@ __global__ __launch_bounds__(kPackThreads) void pack_strided_kernel(StridedArgs 
 
 template <typename CodeT>
 int launch_dense(int32_t dtype, const DenseArgs& a, hipStream_t st) {
+  if (a.E2 == 64 && a.os1 == 1 && a.os2 != 1) {  // 64 heads innermost, positions contiguous out
+    const int64_t grid = (a.R + kTileGroups * 64 - 1) / (kTileGroups * 64);
+    LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
+    switch (dtype) {
+      case LEMA_F32: pack_tile_kernel<LEMA_F32, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+      case LEMA_F16: pack_tile_kernel<LEMA_F16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+      default: pack_tile_kernel<LEMA_BF16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    }
+    return launch_status("pack_tile_kernel");
+  }
   const int64_t grid = (a.R + kPackThreads - 1) / kPackThreads;
   LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
   switch (dtype) {

@@ -60,8 +60,11 @@ def test_pack_golden(dev):
 @pytest.mark.parametrize("D", [1, 8, 24, 32, 33, 63, 64])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("layout", ["contiguous", "projection", "sliced"])
-def test_pack_layouts(dev, D, dtype, layout):
-    B, H, T = 2, 3, 77
+@pytest.mark.parametrize("H", [3, 64])
+def test_pack_layouts(dev, D, dtype, layout, H):
+    """64 heads in the projection layout take the tiled kernel (codes staged per workgroup,
+    77 positions: tiles cross the batch boundary and the last one is partial)."""
+    B, T = 2, 77
     gen = torch.Generator(device="cpu").manual_seed(D * 7 + H)
     specials = torch.tensor([0.0, -0.0, float("nan"), float("inf"), -float("inf")]).to(dtype)
     if layout == "contiguous":
