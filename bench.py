@@ -68,6 +68,17 @@ HBM_PEAK_GBS = 8000.0
 WARM_SECONDS = 0.5      # least untimed warm-up of the prefill workload (clocks settle)
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 LM_CONFIG = dict(vocab_size=50304, depth=24, dim=1536, num_heads=64, dim_ff=6144)
+# The reference's own 0.8B inference geometry (code/experiments/main_inference/run_paper.sh:72,
+# "G08 ... --head-dim 64"; 834,086,400 parameters) and its published LEMA numbers with the
+# host-RAM store on one RTX 3090 (code/experiments/main_inference/out/*.jsonl).
+REF08B_CONFIG = dict(vocab_size=50304, depth=24, dim=1536, num_heads=24, d_qk=64, d_v=64,
+                     dim_ff=4096)
+REF08B_PUBLISHED = {
+    "decode_b1_worst_case_ms_per_token_at_16k": [3.049, "gen_08B_ram.jsonl:11"],
+    "decode_b16_trained_ms_per_token_at_16": [4.280, "genB16_08B_trained_ram.jsonl:1"],
+    "prefill_b1_worst_case_tokens_per_s_at_16384": [19238, "prefill_08B_ram.jsonl:8"],
+    "hardware": "one RTX 3090 + host-RAM store (16 host threads)",
+}
 BYTES_PER_QUERY = 4 + 4 + 4 + 128 + 128
 
 
@@ -83,6 +94,9 @@ def parse():
     ap.add_argument("--dm-batch", type=int, default=16)
     ap.add_argument("--dm-prompt", type=int, default=4096)
     ap.add_argument("--dm-steps", type=int, default=256)
+    ap.add_argument("--dm-geometry", choices=["lm", "ref08b"], default="lm",
+                    help="decode_model geometry: the lm_forward model (64 heads of 24) or the "
+                         "reference's 0.8B inference model (24 heads of 64, SwiGLU 4096)")
     ap.add_argument("--long-calls", type=int, default=16,
                     help="calls of 2^20 positions of the long_context workload to run")
     ap.add_argument("--long-parity-calls", type=int, default=1,
@@ -589,7 +603,7 @@ def bench_decode_model(a):
 
     if not build.LIB.exists():
         build.build()
-    cfg = ModelConfig(**LM_CONFIG)
+    cfg = ModelConfig(**(LM_CONFIG if a.dm_geometry == "lm" else REF08B_CONFIG))
     B, L, steps = a.dm_batch, a.dm_prompt, a.dm_steps
     dev = torch.device("cuda", 0)
     torch.manual_seed(0)
@@ -609,6 +623,12 @@ def bench_decode_model(a):
     prompt = torch.randint(0, 50304, (B, L), generator=g).to(dev)
     stream = torch.cuda.current_stream(dev)
     with torch.no_grad():
+        # a short prefill into a scratch cache first, so the timed one runs warm
+        scratch = model.new_cache("hbm", max_cache_len=64, batch=B,
+                                  codes_hook=worst_case_codes(cfg.depth))
+        model(prompt[:, :64], cache=scratch, return_logits=False)
+        del scratch
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
         model(prompt[:, :-1], cache=cache, return_logits=False)
         torch.cuda.synchronize()
@@ -646,8 +666,11 @@ def bench_decode_model(a):
                    "prompt": L, "store_partitions": P, "store_slots": cache.store.cap,
                    "store_bytes": cache.nbytes(), "entries_after": cache.entries(),
                    "prefill_s": round(t_prefill, 3),
-                   "graph": "one replay per token (all 24 layers and their store exchanges)",
-                   "parallelism": "single GPU"},
+                   "prefill_tokens_per_s": round(B * (L - 1) / t_prefill, 1),
+                   "graph": "one replay per token (all layers and their store exchanges)",
+                   "parallelism": "single GPU",
+                   **({"reference_published": REF08B_PUBLISHED}
+                      if a.dm_geometry == "ref08b" else {})},
         "roofline": {"bound": "hbm (weights read once per step)", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": None, "kernel": "whole decode step",
