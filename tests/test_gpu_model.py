@@ -79,12 +79,13 @@ def test_graph_decoder_with_worst_case_codes(dev):
     assert (c.counts() == 10).all()
 
 
-def test_bf16_token_steps_match_oracle_loss(dev):
+@pytest.mark.parametrize("heads", [8, 4])
+def test_bf16_token_steps_match_oracle_loss(dev, heads):
     """bf16 model stepped one token at a time through the HBM cache -- the decode shapes, where
     the projections, SwiGLU and the residual add run on the skinny MFMA kernels with their
     fused epilogues -- gives the functional oracle's loss on the whole sequence within 1e-2
-    relative."""
-    geo = dict(vocab_size=512, depth=3, dim=256, num_heads=8, dim_ff=512)
+    relative; heads of 32 (32-bit codes) and of 64 (64-bit codes, whole 64-column tiles)."""
+    geo = dict(vocab_size=512, depth=3, dim=256, num_heads=heads, dim_ff=512)
     m, cfg = make(dev, dtype=torch.bfloat16, **geo)
     tok = torch.randint(0, 512, (4, 97), device=dev)
     x, y = tok[:, :-1], tok[:, 1:]
