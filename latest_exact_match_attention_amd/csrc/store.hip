@@ -127,19 +127,45 @@ __device__ __forceinline__ Window window_bits(bool m, bool e, int gbase) {
   const uint64_t mask = G == 64 ? ~0ull : ((1ull << G) - 1);
   return Window{(__ballot(m) >> gbase) & mask, (__ballot(e) >> gbase) & mask};
 }
-template <int G>
-__device__ __forceinline__ Window read_window(const StoreArgs& a, int64_t base, int64_t left,
-                                              uint64_t code, uint64_t tag, int gl, int gbase) {
-  bool m = false, e = false;
+// A lane's slot header of a window (loaded apart from its use, so that other reads can be in
+// flight with it).
+struct SlotHead {
+  uint64_t code, state;
+  bool valid;
+};
+__device__ __forceinline__ SlotHead load_head(const StoreArgs& a, int64_t base, int64_t left,
+                                              int gl) {
+  SlotHead h{0ull, 0ull, false};
   if (gl < left) {
     int64_t s = base + gl;
     if (s >= a.cap) s -= a.cap;
     const uint64_t* hdr = reinterpret_cast<const uint64_t*>(a.table + s * a.stride);
-    const uint64_t st = hdr[1];
-    m = st == tag && hdr[0] == code;
-    e = st == kStateEmpty;
+    h.state = hdr[1];
+    h.code = hdr[0];
+    h.valid = true;
   }
-  return window_bits<G>(m, e, gbase);
+  return h;
+}
+template <int G>
+__device__ __forceinline__ Window head_window(const SlotHead& h, uint64_t code, uint64_t tag,
+                                              int gbase) {
+  return window_bits<G>(h.valid && h.state == tag && h.code == code,
+                        h.valid && h.state == kStateEmpty, gbase);
+}
+// Slots in the window at `base` with `left` slots still to probe: G, or with kAligned the slots
+// up to the end of base's G-aligned group, so that every window after the first covers one
+// whole group (with 64-byte slots and G = 2: one 128-byte line per window, where an unaligned
+// pair of slots straddles two lines every other time). The probe order is the same either way.
+template <int G, bool kAligned>
+__device__ __forceinline__ int64_t window_width(int64_t base, int64_t left) {
+  const int64_t w = kAligned ? G - (base & (G - 1)) : G;
+  return w < left ? w : left;
+}
+template <int G, bool kAligned = false>
+__device__ __forceinline__ Window read_window(const StoreArgs& a, int64_t base, int64_t left,
+                                              uint64_t code, uint64_t tag, int gl, int gbase) {
+  return head_window<G>(load_head(a, base, window_width<G, kAligned>(base, left), gl), code, tag,
+                        gbase);
 }
 
 // The first window read as whole slots (header and value, 16-byte pieces): a hit's value is
@@ -168,11 +194,12 @@ __device__ __forceinline__ Window read_window_slots(const StoreArgs& a, int64_t 
 
 // Slot of (tag, code) or -1 (code/lema/csrc/store.cpp:84-93), starting from window w0 read at
 // `base` with `left` slots still unprobed. Group-uniform.
-template <int G>
+template <int G, bool kAligned = false>
 __device__ int64_t group_lookup(const StoreArgs& a, uint64_t code, uint64_t tag, int64_t base,
                                 int64_t left, Window w0, int gl, int gbase) {
-  for (const int64_t left0 = left; left > 0; left -= G) {
-    const Window w = left == left0 ? w0 : read_window<G>(a, base, left, code, tag, gl, gbase);
+  for (const int64_t left0 = left; left > 0;) {
+    const Window w =
+        left == left0 ? w0 : read_window<G, kAligned>(a, base, left, code, tag, gl, gbase);
     const int fm = w.match ? first_bit(w.match) : G;
     const int fe = w.empty ? first_bit(w.empty) : G;
     if (fm < fe) {
@@ -180,7 +207,9 @@ __device__ int64_t group_lookup(const StoreArgs& a, uint64_t code, uint64_t tag,
       return s >= a.cap ? s - a.cap : s;
     }
     if (w.empty) return -1;
-    base += G;
+    const int64_t width = window_width<G, kAligned>(base, left);
+    left -= width;
+    base += width;
     if (base >= a.cap) base -= a.cap;
   }
   return -1;
@@ -211,12 +240,13 @@ __device__ __forceinline__ int64_t claim_in_window(const StoreArgs& a, uint64_t 
 // at `base` with `left` slots still unprobed: 1 = claimed a new slot, 0 = overwrote the
 // partition's own entry, -1 = probed every slot without room. With `claim_only` the key is
 // known to be absent and only free slots are looked for. Group-uniform.
-template <int G>
+template <int G, bool kAligned = false>
 __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, const uint8_t* value,
                             int64_t base, int64_t left, Window w0, bool claim_only, int gl,
                             int gbase) {
-  for (const int64_t left0 = left; left > 0; left -= G) {
-    const Window w = left == left0 ? w0 : read_window<G>(a, base, left, code, tag, gl, gbase);
+  for (const int64_t left0 = left; left > 0;) {
+    const Window w =
+        left == left0 ? w0 : read_window<G, kAligned>(a, base, left, code, tag, gl, gbase);
     const int fm = (!claim_only && w.match) ? first_bit(w.match) : G;
     if (fm < G && (!w.empty || fm < first_bit(w.empty))) {
       int64_t s = base + fm;
@@ -229,7 +259,9 @@ __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, con
       group_copy<G>(a, a.table + s * a.stride + 16, value, gl);
       return 1;
     }
-    base += G;
+    const int64_t width = window_width<G, kAligned>(base, left);
+    left -= width;
+    base += width;
     if (base >= a.cap) base -= a.cap;
   }
   return -1;
@@ -416,6 +448,98 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
   if (gl == 0 && added > 0) atomicAdd(&a.counts[a.g0 + p], static_cast<unsigned long long>(added));
 }
 
+// ------------------------------------------------------------------ one-lane probes
+// The bulk kernels give each item one lane, which reads the headers of a line-aligned pair of
+// slots itself (window_width<2, true>: the first pair may hold only the home slot): with 64-byte
+// slots a probe step is one 128-byte line, and a wave carries 64 items' round trips.
+struct PairHead {
+  uint64_t c[2], s[2];
+  int width;  // slots of the pair on the probe path, 1 or 2
+};
+
+__device__ __forceinline__ PairHead load_pair(const StoreArgs& a, int64_t base, int64_t left) {
+  PairHead p;
+  p.width = static_cast<int>(window_width<2, true>(base, left));
+  const uint64_t* h0 = reinterpret_cast<const uint64_t*>(a.table + base * a.stride);
+  p.c[0] = h0[0];
+  p.s[0] = h0[1];
+  p.c[1] = 0;
+  p.s[1] = kStateEmpty;
+  if (p.width == 2) {
+    const int64_t b1 = base + 1 >= a.cap ? base + 1 - a.cap : base + 1;
+    const uint64_t* h1 = reinterpret_cast<const uint64_t*>(a.table + b1 * a.stride);
+    p.c[1] = h1[0];
+    p.s[1] = h1[1];
+  }
+  return p;
+}
+
+// Slot of (tag, code) or -1 (code/lema/csrc/store.cpp:84-93), probing from `base` with the
+// first pair already loaded.
+__device__ int64_t lane_lookup(const StoreArgs& a, uint64_t code, uint64_t tag, int64_t base,
+                               PairHead p) {
+  for (int64_t left = a.cap; left > 0;) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (k >= p.width) break;
+      if (p.s[k] == tag && p.c[k] == code) return base + k >= a.cap ? base + k - a.cap : base + k;
+      if (p.s[k] == kStateEmpty) return -1;
+    }
+    left -= p.width;
+    base += p.width;
+    if (base >= a.cap) base -= a.cap;
+    if (left > 0) p = load_pair(a, base, left);
+  }
+  return -1;
+}
+
+// The value of a slot: from registers (`vals`, when the row is at most kSpecPieces 16-byte
+// pieces: a.spec) or copied from `value`.
+__device__ __forceinline__ void lane_put_value(const StoreArgs& a, int64_t s, const uint8_t* value,
+                                               const u32x4 (&vals)[kSpecPieces]) {
+  uint8_t* dst = a.table + s * a.stride + 16;
+  if (a.spec) {
+#pragma unroll
+    for (int k = 0; k < kSpecPieces; ++k)
+      if (k < a.pieces) *reinterpret_cast<u32x4*>(dst + 16 * k) = vals[k];
+  } else {
+    group_copy<1>(a, dst, value, 0);
+  }
+}
+
+// Insert (tag, code) -> value (code/lema/csrc/store.cpp:97-117) from home slot `base`: 1 =
+// claimed a new slot, 0 = overwrote the partition's entry, -1 = probed every slot without room.
+// No other lane inserts the same key at the same time, so a claim lost to a race is another
+// key's slot, and every slot that read free was free before the kernel, so the key cannot lie
+// beyond it: the probe goes on to claim.
+__device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, const uint8_t* value,
+                           const u32x4 (&vals)[kSpecPieces], int64_t base) {
+  PairHead p = load_pair(a, base, a.cap);
+  for (int64_t left = a.cap; left > 0;) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if (k >= p.width) break;
+      const int64_t s = base + k >= a.cap ? base + k - a.cap : base + k;
+      if (p.s[k] == tag && p.c[k] == code) {
+        lane_put_value(a, s, value, vals);
+        return 0;
+      }
+      if (p.s[k] == kStateEmpty &&
+          atomicCAS(reinterpret_cast<unsigned long long*>(state_ptr(a, s)), kStateEmpty, tag) ==
+              kStateEmpty) {
+        *reinterpret_cast<uint64_t*>(a.table + s * a.stride) = code;
+        lane_put_value(a, s, value, vals);
+        return 1;
+      }
+    }
+    left -= p.width;
+    base += p.width;
+    if (base >= a.cap) base -= a.cap;
+    if (left > 0) p = load_pair(a, base, left);
+  }
+  return -1;
+}
+
 // ------------------------------------------------------------------ bulk calls
 // A call with many positions per partition (32-bit codes) runs in sub-calls of up to kBulkSpan
 // positions, each as a few kernels over all of its items at once instead of one launch per
@@ -423,80 +547,87 @@ __global__ __launch_bounds__(kThreads) void store_chunk_kernel(StoreArgs a) {
 //   clear    the scratch group table;
 //   chunks   one workgroup per (partition, 1024-chunk): in-chunk answers of the queries (LDS
 //            resolver), the chunk's key summary (code -> latest position, the LDS table written
-//            out), and every distinct key code entered in the group table under
-//            (partition + 1) << 32 | code -- one 64-bit CAS, no half-written key -- with the
-//            chunk's bit in the code's 64-bit chunk mask and its latest position (atomicMax);
+//            out), and every distinct key code entered in the partition's region of the group
+//            table with the chunk's bit in its chunk mask: one 64-bit CAS (claim) or OR (the
+//            code is there) per code and chunk;
 //   queries  a query without an in-chunk answer takes the highest chunk below its own in its
 //            code's mask and that chunk's summary gives the key; with no such chunk it looks
 //            the store up (the table still holds exactly the keys before the sub-call);
-//   insert   every (partition, code) of the sub-call writes the value of its latest key over
-//            its existing store entry or claims a slot (code 0 in a kernel of its own, see
-//            bulk_insert_kernel); a last pass counts the claims per partition.
+//   insert   every (partition, code) of the sub-call takes its latest key from the summary of
+//            the highest chunk in its mask and writes that value over its existing store entry
+//            or claims a slot (code 0 in a kernel of its own, see bulk_insert_kernel); the
+//            claims are counted per partition on the way.
 // The kernel boundary orders every lookup of the sub-call before its inserts.
-constexpr int kBulkSpan = 64 * kChunk;  // positions per sub-call: chunk masks fit 64 bits
+constexpr int kBulkSpan = 32 * kChunk;  // positions per sub-call: chunk masks fit 32 bits
 static_assert((kSlots & (kSlots - 1)) == 0, "chunk summaries are probed with a slot mask");
 constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots, the sentinel's
 
-// One (partition, code) of a sub-call: 32 bytes, so the claim and both updates of a chunk's
-// entry touch a single cache line.
-struct GroupSlot {
-  uint64_t key;    // (partition + 1) << 32 | code, 0 = free
-  uint64_t mask;   // bit c: chunk c of the sub-call holds keys with this code
-  int32_t last;    // latest key position of the code in the sub-call
-  int32_t flag;    // 2: claimed a store slot in this sub-call
-  uint64_t pad;
-};
-
+// Group table: a region of `cap` 64-bit words per partition, open addressing with linear probing
+// inside the region. A word is code | mask << 32 (bit c of the mask: chunk c of the sub-call
+// holds keys with this code) or 0 for a free word; an entered word always has a mask bit set.
 struct BulkWs {
-  GroupSlot* gt;
-  int64_t* zero_slot;  // per partition: group slot of code 0, or -1
-  uint32_t* sum_code;  // per (partition, chunk): the kSlots key-code slots
-  int32_t* sum_pos;    // per (partition, chunk): kSumPos latest positions
-  int32_t* src_in;     // per query of the sub-call: in-chunk answer (sub-call position) or -1
-  int64_t gt_cap;      // power of two
-  int32_t nch;         // chunks per partition in the sub-call
+  unsigned long long* gt;  // P regions of cap words
+  int64_t* zero_slot;      // per partition: word of code 0, or -1
+  uint32_t* sum_code;      // per (partition, chunk): the kSlots key-code slots
+  int32_t* sum_pos;        // per (partition, chunk): kSumPos latest positions
+  int32_t* src_in;         // per query of the sub-call: in-chunk answer (sub-call position) or -1
+  uint32_t* claims;        // per workgroup of bulk_insert_kernel: store slots it claimed
+  int32_t cap;             // words per region: a power of two, at least twice kBulkSpan
+  int32_t cap_log2;
+  int32_t nch;             // chunks per partition in the sub-call
 };
 
-__device__ __forceinline__ int64_t gt_home(uint64_t key, int64_t cap) {
-  return static_cast<int64_t>(splitmix_fin(key) & static_cast<uint64_t>(cap - 1));
+__device__ __forceinline__ int32_t gt_home(uint32_t code, int32_t cap) {
+  return static_cast<int32_t>(splitmix_fin(code) & static_cast<uint64_t>(cap - 1));
 }
 
-// Find or enter U keys in the group table (one thread; the table is at most half full): the
-// slots, -1 for an inactive key or one that found no room. The keys' probes advance together,
-// so each round's reads, then its CASes, are in flight at once.
+__device__ __forceinline__ uint32_t gt_code(unsigned long long word) {
+  return static_cast<uint32_t>(word);
+}
+
+// Enter U codes of chunk `bit` in region r (one thread; the region is at most half full): a free
+// word is claimed with the code and the bit by one CAS, a word of the code gets the bit by one
+// OR. The codes' probes advance together, so each round's reads, then its atomics, are in flight
+// at once. A word once entered keeps its code, so a read that shows a code is never stale in the
+// code; a read of 0 may be, and the CAS then returns the word that won. g: the words' indices,
+// -1 for an inactive code or one that found no room.
 template <int U>
-__device__ __forceinline__ void gt_claim(const BulkWs& w, const uint64_t (&key)[U],
-                                         const bool (&act)[U], int64_t (&g)[U]) {
-  int64_t sl[U], left[U];
+__device__ __forceinline__ void gt_enter(const BulkWs& w, int64_t r, const uint32_t (&code)[U],
+                                         const bool (&act)[U], int c, int64_t (&g)[U]) {
+  unsigned long long* region = w.gt + (r << w.cap_log2);
+  const unsigned long long bit = 1ull << (32 + c);
+  int32_t sl[U], left[U];
   bool todo[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    sl[u] = gt_home(key[u], w.gt_cap);
-    left[u] = w.gt_cap;
+    sl[u] = gt_home(code[u], w.cap);
+    left[u] = w.cap;
     todo[u] = act[u];
     g[u] = -1;
   }
   for (;;) {
     bool any = false;
-    uint64_t k[U];
+    unsigned long long k[U], old[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) k[u] = todo[u] ? w.gt[sl[u]].key : 0ull;
-    unsigned long long old[U];
+    for (int u = 0; u < U; ++u) k[u] = todo[u] ? region[sl[u]] : 0ull;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      old[u] = 1ull;  // not a claim
+      old[u] = k[u];
       if (todo[u] && k[u] == 0)
-        old[u] = atomicCAS(reinterpret_cast<unsigned long long*>(&w.gt[sl[u]].key), 0ull,
-                           static_cast<unsigned long long>(key[u]));
+        old[u] = atomicCAS(&region[sl[u]], 0ull, bit | code[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!todo[u]) continue;
-      if (k[u] == key[u] || (k[u] == 0 && (old[u] == 0 || old[u] == key[u]))) {
-        g[u] = sl[u];  // found, claimed, or claimed by a twin of this key first
+      if (old[u] == 0) {  // claimed, the bit with it
+        g[u] = (r << w.cap_log2) + sl[u];
         todo[u] = false;
-      } else {         // the slot holds another key (seen, or won by it first): the next
-        sl[u] = (sl[u] + 1) & (w.gt_cap - 1);
+      } else if (gt_code(old[u]) == code[u]) {  // the code's word
+        atomicOr(&region[sl[u]], bit);
+        g[u] = (r << w.cap_log2) + sl[u];
+        todo[u] = false;
+      } else {  // another code's word
+        sl[u] = (sl[u] + 1) & (w.cap - 1);
         if (--left[u] == 0) todo[u] = false;
       }
       any = any || todo[u];
@@ -505,35 +636,42 @@ __device__ __forceinline__ void gt_claim(const BulkWs& w, const uint64_t (&key)[
   }
 }
 
-// Slot of `key` in the group table or -1, kGroup lanes probing kGroup slots per read.
-__device__ __forceinline__ int64_t gt_find_group(const BulkWs& w, uint64_t key, int gl, int gbase) {
-  int64_t base = gt_home(key, w.gt_cap);
-  for (int64_t left = w.gt_cap; left > 0; left -= kGroup) {
-    const uint64_t k = w.gt[(base + gl) & (w.gt_cap - 1)].key;
-    const Window win = window_bits<kGroup>(k == key, k == 0, gbase);
-    const int fm = win.match ? first_bit(win.match) : kGroup;
-    const int fe = win.empty ? first_bit(win.empty) : kGroup;
-    if (fm < fe) return (base + fm) & (w.gt_cap - 1);
-    if (win.empty) return -1;
-    base = (base + kGroup) & (w.gt_cap - 1);
-  }
-  return -1;
+// The word at `code`'s home in region r (loaded apart from its use).
+__device__ __forceinline__ unsigned long long gt_first_word(const BulkWs& w, int64_t r,
+                                                           uint32_t code) {
+  return w.gt[(r << w.cap_log2) + gt_home(code, w.cap)];
 }
 
-// Latest position of `code` in a chunk summary (the code is known to be there), kGroup lanes
-// reading kGroup consecutive slots (two 4-slot buckets) per step.
+// The word of `code` in region r of the group table, or 0; k0 is the word at its home.
+__device__ __forceinline__ unsigned long long gt_word(const BulkWs& w, int64_t r, uint32_t code,
+                                                     unsigned long long k0) {
+  const unsigned long long* region = w.gt + (r << w.cap_log2);
+  int32_t s = gt_home(code, w.cap);
+  unsigned long long k = k0;
+  for (int32_t left = w.cap; left > 0; --left) {
+    if (k == 0 || gt_code(k) == code) return k;
+    s = (s + 1) & (w.cap - 1);
+    k = region[s];
+  }
+  return 0;
+}
+
+// Latest position of `code` in a chunk summary, or -1: the image of the chunk's LDS table
+// (4-slot buckets from bucket_of, linear probing), read a bucket (16 bytes) at a time; the
+// code's slot comes before any free slot on its probe path.
 __device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int32_t* pos,
-                                                uint32_t code, int gl, int gbase) {
-  if (code == sentinel<uint32_t>()) return pos[kSlots];
-  int base = 4 * bucket_of<kBuckets>(fold(code));
-  for (int left = kSlots; left > 0; left -= kGroup) {
-    const uint32_t c = codes[(base + gl) & (kSlots - 1)];
-    const Window win = window_bits<kGroup>(c == code, c == sentinel<uint32_t>(), gbase);
-    const int fm = win.match ? first_bit(win.match) : kGroup;
-    const int fe = win.empty ? first_bit(win.empty) : kGroup;
-    if (fm < fe) return pos[(base + fm) & (kSlots - 1)];
-    if (win.empty) return -1;
-    base = (base + kGroup) & (kSlots - 1);
+                                                uint32_t code) {
+  const uint32_t SENT = sentinel<uint32_t>();
+  if (code == SENT) return pos[kSlots];
+  int b = bucket_of<kBuckets>(fold(code));
+  for (int left = kBuckets; left > 0; --left) {
+    const u32x4 e = *reinterpret_cast<const u32x4*>(codes + 4 * b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (e[i] == code) return pos[4 * b + i];
+      if (e[i] == SENT) return -1;
+    }
+    b = (b + 1) & (kBuckets - 1);
   }
   return -1;
 }
@@ -541,8 +679,9 @@ __device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int
 __global__ __launch_bounds__(256) void bulk_clear_kernel(BulkWs w, int64_t P) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const int64_t i0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  for (int64_t i = i0; i < w.gt_cap; i += stride)
-    w.gt[i] = GroupSlot{0ull, 0ull, -1, 0, 0ull};
+  const int64_t words = P << w.cap_log2;
+  ulonglong2* gt2 = reinterpret_cast<ulonglong2*>(w.gt);
+  for (int64_t i = i0; i < words / 2; i += stride) gt2[i] = ulonglong2{0ull, 0ull};
   for (int64_t i = i0; i < P; i += stride) w.zero_slot[i] = -1;
 }
 
@@ -600,142 +739,129 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
   int32_t* spos = w.sum_pos + sum * kSumPos;
   for (int x = t; x < kSlots; x += kThreads) scode[x] = s.code[x];
   for (int x = t; x <= kSlots; x += kThreads) spos[x] = s.pos[x];
-  constexpr int U = 4;  // codes per thread whose claims overlap
+  constexpr int U = 4;  // codes per thread whose probes overlap
   for (int x0 = t; x0 <= kSlots; x0 += U * kThreads) {
-    int32_t lp[U];
     uint32_t code[U];
-    uint64_t key[U];
     bool act[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int x = x0 + u * kThreads;
-      lp[u] = x <= kSlots ? s.pos[x] : -1;
+      act[u] = x <= kSlots && s.pos[x] >= 0;
       code[u] = x < kSlots ? s.code[x] : SENT;
-      key[u] = (static_cast<uint64_t>(p + 1) << 32) | code[u];
-      act[u] = lp[u] >= 0;
     }
     int64_t g[U];
-    gt_claim<U>(w, key, act, g);
+    gt_enter<U>(w, p, code, act, c, g);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (!act[u]) continue;
-      if (g[u] < 0) {  // cannot happen with the table at most half full; fail loudly
+      if (g[u] < 0)  // cannot happen with the region at most half full; fail loudly
         atomicOr(a.full, 2);
-        continue;
-      }
-      atomicOr(reinterpret_cast<unsigned long long*>(&w.gt[g[u]].mask), 1ull << c);
-      atomicMax(&w.gt[g[u]].last, c * kChunk + lp[u]);
-      if (code[u] == 0) w.zero_slot[p] = g[u];
+      else if (code[u] == 0)
+        w.zero_slot[p] = g[u];
     }
   }
 }
 
+// One lane per query of the sub-call.
 __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t i = gid / kGroup;  // query of the sub-call: partition i / len, position i % len
-  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t n = static_cast<int64_t>(a.n / a.T) * a.len;
-  if (i >= n) return;
+  if (i >= n) return;  // partition i / len, position i % len
   const int64_t p = i / a.len;
   const int o = static_cast<int>(i - p * a.len);
   const int64_t base = p * a.T + a.s0;  // item of the sub-call's position 0
   uint8_t* dst = a.out + (base + o) * a.vbytes;
   int32_t j = w.src_in[i];
+  const uint32_t code = static_cast<const uint32_t*>(a.qc)[base + o];
   if (j < 0) {
-    const uint32_t code = static_cast<const uint32_t*>(a.qc)[base + o];
+    // the group table's and the store's first reads are in flight together: most queries
+    // without an in-chunk answer end in the store
+    const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
+    const int64_t h = home_slot(code, tag - 2, a.cap);
+    const PairHead first = load_pair(a, h, a.cap);
+    const unsigned long long word = gt_word(w, p, code, gt_first_word(w, p, code));
     const int c = o / kChunk;
-    const int64_t g = gt_find_group(w, (static_cast<uint64_t>(p + 1) << 32) | code, gl, gbase);
-    const uint64_t m = g >= 0 ? (w.gt[g].mask & ((1ull << c) - 1)) : 0;
+    const uint32_t m = static_cast<uint32_t>(word >> 32) & ((1u << c) - 1u);
     if (m) {
-      const int c2 = 63 - __clzll(m);
+      const int c2 = 31 - __clz(m);
       const int64_t sum = p * w.nch + c2;
-      const int32_t lp = summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code,
-                                      gl, gbase);
+      const int32_t lp = summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code);
       j = lp >= 0 ? c2 * kChunk + lp : -1;
     }
     if (j < 0) {
-      const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-      const int64_t h = home_slot(code, tag - 2, a.cap);
-      const int64_t sl = group_lookup<kGroup>(
-          a, code, tag, h, a.cap, read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), gl, gbase);
-      group_copy<kGroup>(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, gl);
+      const int64_t sl = lane_lookup(a, code, tag, h, first);
+      group_copy<1>(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, 0);
       return;
     }
   }
-  group_copy<kGroup>(a, dst, a.values + (base + j) * a.vbytes, gl);
+  group_copy<1>(a, dst, a.values + (base + j) * a.vbytes, 0);
 }
 
-// Every (partition, code) of the sub-call, once: overwrite its store entry with the value of
-// its latest key, or claim a slot. The lookups of this sub-call are over (previous kernel), and
-// no other item looks for the same key, so the only thing a concurrent claim can be mistaken
-// for is code 0 (a claimed slot whose code is not written yet reads as 0): code-0 keys wait
-// for bulk_zero_kernel.
-__device__ __forceinline__ void bulk_insert_group(const StoreArgs& a, const BulkWs& w, int64_t g,
-                                                  int gl, int gbase) {
-  const uint64_t key = w.gt[g].key;
-  const int64_t p = static_cast<int64_t>(key >> 32) - 1;
-  const uint64_t code = key & 0xFFFFFFFFull;
+// Word g of the group table (partition p): the value of its code's latest key in the sub-call
+// over the code's existing store entry, or into a claimed slot. The lookups of this sub-call are
+// over (previous kernel), and no other item looks for the same key, so the only thing a
+// concurrent claim can be mistaken for is code 0 (a claimed slot whose code is not written yet
+// reads as 0): code-0 keys wait for bulk_zero_kernel. Returns 1 for a claim.
+__device__ __forceinline__ int bulk_insert_word(const StoreArgs& a, const BulkWs& w, int64_t p,
+                                                unsigned long long word) {
+  const uint32_t code = gt_code(word);
+  const int c2 = 31 - __clz(static_cast<uint32_t>(word >> 32));
+  const int64_t sum = p * w.nch + c2;
+  const int32_t lp = summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code);
+  if (lp < 0) {  // the summary of a chunk in the mask holds the code; fail loudly
+    atomicOr(a.full, 2);
+    return 0;
+  }
   const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-  const int64_t h = home_slot(code, tag - 2, a.cap);
-  const uint8_t* v = a.values + (p * a.T + a.s0 + w.gt[g].last) * a.vbytes;
-  const int r = group_insert<kGroup>(a, code, tag, v, h, a.cap,
-                                     read_window<kGroup>(a, h, a.cap, code, tag, gl, gbase), false,
-                                     gl, gbase);
-  if (gl == 0) {
-    if (r > 0) w.gt[g].flag = 2;
-    if (r < 0) atomicOr(a.full, 1);
-  }
+  const uint8_t* v = a.values + (p * a.T + a.s0 + c2 * kChunk + lp) * a.vbytes;
+  u32x4 vals[kSpecPieces];  // the value row, loaded with the first probe
+#pragma unroll
+  for (int k = 0; k < kSpecPieces; ++k)
+    vals[k] = a.spec && k < a.pieces ? *reinterpret_cast<const u32x4*>(v + 16 * k)
+                                     : u32x4{0u, 0u, 0u, 0u};
+  const int r = lane_insert(a, code, tag, v, vals, home_slot(code, tag - 2, a.cap));
+  if (r < 0) atomicOr(a.full, 1);
+  return r > 0 ? 1 : 0;
 }
 
+// One lane per word of the group table. A workgroup's words lie in one region (regions are at
+// least 1024 words); it writes its number of claims to `claims`, and bulk_zero_kernel adds a
+// region's numbers to the partition's count once: the region's workgroups run close together in
+// time, so atomics on the partition's count would serialise.
 __global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t g = gid / kGroup;
-  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
-  if (g >= w.gt_cap) return;
-  const uint64_t key = w.gt[g].key;
-  if (key == 0 || (key & 0xFFFFFFFFull) == 0) return;
-  bulk_insert_group(a, w, g, gl, gbase);
+  __shared__ uint32_t n_claims;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (threadIdx.x == 0) n_claims = 0;
+  __syncthreads();
+  const unsigned long long word = w.gt[g];
+  int claimed = 0;
+  if (word != 0 && gt_code(word) != 0) claimed = bulk_insert_word(a, w, g >> w.cap_log2, word);
+  const unsigned long long b = __ballot(claimed);
+  if ((threadIdx.x & 63) == 0 && b != 0) atomicAdd(&n_claims, static_cast<uint32_t>(__popcll(b)));
+  __syncthreads();
+  if (threadIdx.x == 0) w.claims[blockIdx.x] = n_claims;
 }
 
-__global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, int64_t P) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t p = gid / kGroup;
-  const int lane = threadIdx.x & 63, gl = lane % kGroup, gbase = lane - gl;
-  if (p >= P) return;
+// One workgroup per partition: the insert of code 0, then the partition's claims of the
+// sub-call (its region's workgroup numbers, and code 0's) added to its count.
+__global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, int32_t blocks_per_region) {
+  __shared__ uint32_t total;
+  const int64_t p = blockIdx.x;
+  const int t = threadIdx.x;
+  if (t == 0) total = 0;
+  __syncthreads();
   const int64_t g = w.zero_slot[p];
-  if (g < 0) return;
-  bulk_insert_group(a, w, g, gl, gbase);
-}
-
-// Claims per partition: a contiguous range of the group table per workgroup, counted in LDS
-// (up to kCountParts partitions) and added to counts once per partition and workgroup.
-constexpr int kCountParts = 4096;
-__global__ __launch_bounds__(256) void bulk_count_kernel(StoreArgs a, BulkWs w, int64_t span) {
-  __shared__ uint32_t hist[kCountParts];
-  const int64_t P = a.n / a.T;
-  const bool local = P <= kCountParts;
-  if (local)
-    for (int x = threadIdx.x; x < P; x += blockDim.x) hist[x] = 0;
+  if (t == 0 && g >= 0 && bulk_insert_word(a, w, p, w.gt[g])) atomicAdd(&total, 1u);
+  uint32_t sum = 0;
+  for (int i = t; i < blocks_per_region; i += blockDim.x) sum += w.claims[p * blocks_per_region + i];
+  if (sum) atomicAdd(&total, sum);
   __syncthreads();
-  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * span;
-  const int64_t g1 = g0 + span < w.gt_cap ? g0 + span : w.gt_cap;
-  for (int64_t g = g0 + threadIdx.x; g < g1; g += blockDim.x) {
-    if (w.gt[g].flag != 2) continue;
-    const int64_t p = static_cast<int64_t>(w.gt[g].key >> 32) - 1;
-    if (local)
-      atomicAdd(&hist[p], 1u);
-    else
-      atomicAdd(&a.counts[a.g0 + p], 1ull);
-  }
-  __syncthreads();
-  if (local)
-    for (int x = threadIdx.x; x < P; x += blockDim.x)
-      if (hist[x]) atomicAdd(&a.counts[a.g0 + x], static_cast<unsigned long long>(hist[x]));
+  if (t == 0 && total) atomicAdd(&a.counts[a.g0 + p], static_cast<unsigned long long>(total));
 }
 
 // Workspace layout of a bulk call of P partitions (sub-calls of S positions).
 struct BulkLayout {
-  int64_t gt_cap, nch, off_zero, off_scode, off_spos, off_src, bytes;
+  int64_t cap, cap_log2, nch, off_zero, off_scode, off_spos, off_src, off_claims, bytes;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -743,11 +869,14 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 BulkLayout bulk_layout(int64_t P, int64_t T) {
   BulkLayout L{};
   const int64_t S = T < kBulkSpan ? T : kBulkSpan;
-  int64_t cap = 1024;
-  while (cap < 2 * P * S) cap <<= 1;
-  L.gt_cap = cap;
+  L.cap = 1024;
+  L.cap_log2 = 10;
+  while (L.cap < 2 * S) {
+    L.cap <<= 1;
+    ++L.cap_log2;
+  }
   L.nch = (S + kChunk - 1) / kChunk;
-  int64_t o = align256(cap * static_cast<int64_t>(sizeof(GroupSlot)));
+  int64_t o = align256(P * L.cap * 8);
   L.off_zero = o;
   o += align256(P * 8);
   L.off_scode = o;
@@ -756,6 +885,8 @@ BulkLayout bulk_layout(int64_t P, int64_t T) {
   o += align256(P * L.nch * kSumPos * 4);
   L.off_src = o;
   o += align256(P * S * 4);
+  L.off_claims = o;
+  o += align256(P * L.cap / 256 * 4);
   L.bytes = o;
   return L;
 }
@@ -779,15 +910,15 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
                (long long)ws_bytes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   BulkWs w{};
-  w.gt = reinterpret_cast<GroupSlot*>(ws);
+  w.gt = reinterpret_cast<unsigned long long*>(ws);
   w.zero_slot = reinterpret_cast<int64_t*>(ws + L.off_zero);
   w.sum_code = reinterpret_cast<uint32_t*>(ws + L.off_scode);
   w.sum_pos = reinterpret_cast<int32_t*>(ws + L.off_spos);
   w.src_in = reinterpret_cast<int32_t*>(ws + L.off_src);
-  w.gt_cap = L.gt_cap;
-  const int64_t slot_grid = (L.gt_cap * kGroup + 255) / 256;
-  const int64_t count_blocks = 1024;
-  const int64_t span = (L.gt_cap + count_blocks - 1) / count_blocks;
+  w.claims = reinterpret_cast<uint32_t*>(ws + L.off_claims);
+  w.cap = static_cast<int32_t>(L.cap);
+  w.cap_log2 = static_cast<int32_t>(L.cap_log2);
+  const int32_t blocks_per_region = static_cast<int32_t>(L.cap / 256);  // whole: cap >= 1024
   for (int64_t s0 = 0; s0 < a.T; s0 += kBulkSpan) {
     a.s0 = s0;
     a.len = static_cast<int32_t>(a.T - s0 < kBulkSpan ? a.T - s0 : kBulkSpan);
@@ -797,15 +928,13 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
     bulk_chunk_kernel<<<dim3(P * w.nch), dim3(kThreads), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_chunk_kernel")) return rc;
     if (a.qc != nullptr) {
-      bulk_query_kernel<<<dim3((P * a.len * kGroup + 255) / 256), dim3(256), 0, st>>>(a, w);
+      bulk_query_kernel<<<dim3((P * a.len + 255) / 256), dim3(256), 0, st>>>(a, w);
       if (int rc = launch_status("bulk_query_kernel")) return rc;
     }
-    bulk_insert_kernel<<<dim3(slot_grid), dim3(256), 0, st>>>(a, w);
+    bulk_insert_kernel<<<dim3(P * blocks_per_region), dim3(256), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_insert_kernel")) return rc;
-    bulk_zero_kernel<<<dim3((P * kGroup + 255) / 256), dim3(256), 0, st>>>(a, w, P);
+    bulk_zero_kernel<<<dim3(P), dim3(256), 0, st>>>(a, w, blocks_per_region);
     if (int rc = launch_status("bulk_zero_kernel")) return rc;
-    bulk_count_kernel<<<dim3(count_blocks), dim3(256), 0, st>>>(a, w, span);
-    if (int rc = launch_status("bulk_count_kernel")) return rc;
   }
   return LEMA_OK;
 }

@@ -200,7 +200,7 @@ def test_decode_steps_in_a_graph_equal_eager(dev):
 
 
 # ------------------------------------------------------------------ the bulk path
-# Calls with int32 codes and T > 2048 run as sub-calls of up to 65536 positions with in-chunk
+# Calls with int32 codes and T > 2048 run as sub-calls of up to 32768 positions with in-chunk
 # resolution, per-chunk key summaries and a scratch table of the sub-call's (partition, code)
 # pairs: the results must be the dict's in every case the chunked path covers.
 
@@ -212,8 +212,8 @@ def test_bulk_one_shot_and_continued(dev):
 
 
 def test_bulk_crosses_a_sub_call(dev):
-    """T = 70,000: a sub-call of 65,536 positions and one of 4,464, in order; codes repeat
-    across the boundary."""
+    """T = 70,000: sub-calls of 32,768, 32,768 and 4,464 positions, in order; codes repeat
+    across the boundaries."""
     run_dict_case(dev, seed=12, P=2, T=70_000, chunk=70_000, n_codes=20_000,
                   capacity=100_000, code_dtype=torch.int32)
 
@@ -246,6 +246,58 @@ def test_bulk_sentinel_and_zero_codes(dev):
     assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want)
     assert np.array_equal(store.counts.numpy(), ref.counts())
     assert set(store.dump()[1].cpu().numpy().tolist()) == {0xFFFFFFFF, 0, 1, 2, 3}
+
+
+def test_bulk_region_at_design_load(dev):
+    """Whole sub-calls of distinct key codes, so each partition's region of the scratch table
+    holds 32,768 codes (half full, its design limit), and queries that copy the key 1 to
+    40,000 positions back (in the chunk, in an earlier chunk, in the previous sub-call) or
+    miss."""
+    rng = np.random.default_rng(17)
+    P, T = 2, 65_536
+    # an odd multiplier is a bijection modulo 2^30: distinct codes below 2^30
+    kc = (np.arange(P * T, dtype=np.int64) * 2_654_435_761) % (1 << 30)
+    qc = rng.integers(0, 1 << 30, size=P * T, dtype=np.int64)
+    pos = np.arange(P * T) % T
+    back = pos - rng.integers(1, 40_001, size=P * T)
+    copy = (rng.random(P * T) < 0.5) & (back >= 0)
+    qc[copy] = kc[(np.arange(P * T) - pos + back)[copy]]
+    vals = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=400_000, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+    store.exchange(torch.from_numpy(qc).to(dev).to(torch.int32),
+                   torch.from_numpy(kc).to(dev).to(torch.int32),
+                   torch.from_numpy(vals.view(np.int16)).to(dev), out, T, 0)
+    want = ref.exchange(qc, kc, vals.view(np.uint8).reshape(-1, 2 * D_V), T, 0)
+    got = out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V)
+    assert np.array_equal(got, want)
+    assert (got != 0).any(-1).mean() > 0.3   # about 0.35 of the queries copy an earlier key
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    store.check_full()
+
+
+@pytest.mark.parametrize("d_v", [32, 40, 64])
+def test_bulk_long_value_rows(dev, d_v):
+    """Rows of 64, 80 and 128 bytes through two long calls: up to four 16-byte pieces a key's
+    value row is held in registers while its slot is found, beyond that it is copied."""
+    run_store_rows_case(dev, seed=100 + d_v, d_v=d_v, P=3, Ts=(5000, 2600))
+
+
+def run_store_rows_case(dev, seed, d_v, P, Ts):
+    rng = np.random.default_rng(seed)
+    store = HashStore(d_v, groups=P, dtype=np.uint16, capacity=60_000, device=dev)
+    ref = oracle.DictStore(P, 2 * d_v)
+    for T in Ts:
+        qc = rng.integers(0, 2000, P * T)
+        kc = rng.integers(0, 2000, P * T)
+        v = rng.integers(0, 256, size=(P * T, 2 * d_v), dtype=np.uint8)
+        out = torch.empty((P * T, 2 * d_v), dtype=torch.uint8, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev).to(torch.int32),
+                       torch.from_numpy(kc).to(dev).to(torch.int32),
+                       torch.from_numpy(v).to(dev), out, T, 0)
+        assert np.array_equal(out.cpu().numpy(), ref.exchange(qc, kc, v, T, 0)), T
+    assert np.array_equal(store.counts.numpy(), ref.counts())
 
 
 def test_bulk_equals_chunked_path_and_insert_only(dev):
@@ -282,9 +334,9 @@ def test_bulk_equals_chunked_path_and_insert_only(dev):
 
 
 def test_bulk_many_partitions_equals_chunked_path(dev):
-    """4,200 partitions (more than the count kernel's LDS histogram holds) x T = 2,100: the
-    bulk path (int32 codes) and the chunked path (int64 codes) agree on outputs, entries and
-    per-partition counts."""
+    """4,200 partitions x T = 2,100 (4,200 regions of the scratch table, each partition's
+    claims tallied from its region's workgroups): the bulk path (int32 codes) and the chunked
+    path (int64 codes) agree on outputs, entries and per-partition counts."""
     rng = np.random.default_rng(16)
     P, T, cap = 4200, 2100, 9_000_000
     qc = rng.integers(0, 700, size=P * T)
