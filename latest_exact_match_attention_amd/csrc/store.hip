@@ -544,12 +544,12 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, cons
 // A call with many positions per partition (32-bit codes) runs in sub-calls of up to kBulkSpan
 // positions, each as a few kernels over all of its items at once instead of one launch per
 // 1024-position sub-chunk:
-//   clear    the scratch group table;
 //   chunks   one workgroup per (partition, 1024-chunk): in-chunk answers of the queries (LDS
-//            resolver), the chunk's key summary (code -> latest position, the LDS table written
-//            out), and every distinct key code entered in the partition's region of the group
-//            table with the chunk's bit in its chunk mask: one 64-bit CAS (claim) or OR (the
-//            code is there) per code and chunk;
+//            resolver) and the chunk's key summary (code -> latest position, the LDS table
+//            written out);
+//   table    one workgroup per (partition, quarter of the code hash space): the quarter's codes
+//            of every chunk summary entered in an LDS table, code -> mask of the chunks holding
+//            keys with it, written out as that quarter of the partition's group table;
 //   queries  a query without an in-chunk answer takes the highest chunk below its own in its
 //            code's mask and that chunk's summary gives the key; with no such chunk it looks
 //            the store up (the table still holds exactly the keys before the sub-call);
@@ -557,101 +557,54 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, cons
 //            the highest chunk in its mask and writes that value over its existing store entry
 //            or claims a slot (code 0 in a kernel of its own, see bulk_insert_kernel); the
 //            claims are counted per partition on the way.
-// The kernel boundary orders every lookup of the sub-call before its inserts.
+// The kernel boundary orders every lookup of the sub-call before its inserts. A quarter with
+// more codes than its LDS table takes (only codes chosen to collide in the hash get there) is
+// marked spilled: its queries and inserts then search the chunk summaries themselves.
 constexpr int kBulkSpan = 32 * kChunk;  // positions per sub-call: chunk masks fit 32 bits
 static_assert((kSlots & (kSlots - 1)) == 0, "chunk summaries are probed with a slot mask");
 constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots, the sentinel's
+constexpr int kQuarters = 4;            // group-table quarters per partition
+constexpr int kQuarterMax = 16384;      // words of a quarter: the LDS table (128 KB)
+constexpr int kTableThreads = 1024;
 
-// Group table: a region of `cap` 64-bit words per partition, open addressing with linear probing
-// inside the region. A word is code | mask << 32 (bit c of the mask: chunk c of the sub-call
-// holds keys with this code) or 0 for a free word; an entered word always has a mask bit set.
+// Group table: per partition `cap` 64-bit words, kQuarters quarters of `sub` words; a code
+// lives in the quarter given by the top bits of its hash, at the slot given by the low bits,
+// with linear probing inside the quarter. A word is code | mask << 32 (bit c of the mask: chunk
+// c of the sub-call holds keys with this code) or 0 for a free word; an entered word always has
+// a mask bit set.
 struct BulkWs {
-  unsigned long long* gt;  // P regions of cap words
+  unsigned long long* gt;  // P x cap words
+  int32_t* spilled;        // per (partition, quarter): 1 = the quarter's table was not built
   int64_t* zero_slot;      // per partition: word of code 0, or -1
   uint32_t* sum_code;      // per (partition, chunk): the kSlots key-code slots
   int32_t* sum_pos;        // per (partition, chunk): kSumPos latest positions
   int32_t* src_in;         // per query of the sub-call: in-chunk answer (sub-call position) or -1
+  uint32_t* qlist;         // per (partition, chunk, quarter): the chunk's distinct key codes
+                           // of the quarter, up to kChunk
+  int32_t* qcount;         // per (partition, chunk, quarter): their number
   uint32_t* claims;        // per workgroup of bulk_insert_kernel: store slots it claimed
-  int32_t cap;             // words per region: a power of two, at least twice kBulkSpan
+  int32_t cap;             // words per partition: a power of two, at least twice kBulkSpan
   int32_t cap_log2;
+  int32_t sub;             // words per quarter: cap / kQuarters
   int32_t nch;             // chunks per partition in the sub-call
 };
 
-__device__ __forceinline__ int32_t gt_home(uint32_t code, int32_t cap) {
-  return static_cast<int32_t>(splitmix_fin(code) & static_cast<uint64_t>(cap - 1));
-}
+__device__ __forceinline__ int gt_quarter(uint64_t h) { return static_cast<int>(h >> 62); }
 
 __device__ __forceinline__ uint32_t gt_code(unsigned long long word) {
   return static_cast<uint32_t>(word);
 }
 
-// Enter U codes of chunk `bit` in region r (one thread; the region is at most half full): a free
-// word is claimed with the code and the bit by one CAS, a word of the code gets the bit by one
-// OR. The codes' probes advance together, so each round's reads, then its atomics, are in flight
-// at once. A word once entered keeps its code, so a read that shows a code is never stale in the
-// code; a read of 0 may be, and the CAS then returns the word that won. g: the words' indices,
-// -1 for an inactive code or one that found no room.
-template <int U>
-__device__ __forceinline__ void gt_enter(const BulkWs& w, int64_t r, const uint32_t (&code)[U],
-                                         const bool (&act)[U], int c, int64_t (&g)[U]) {
-  unsigned long long* region = w.gt + (r << w.cap_log2);
-  const unsigned long long bit = 1ull << (32 + c);
-  int32_t sl[U], left[U];
-  bool todo[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    sl[u] = gt_home(code[u], w.cap);
-    left[u] = w.cap;
-    todo[u] = act[u];
-    g[u] = -1;
-  }
-  for (;;) {
-    bool any = false;
-    unsigned long long k[U], old[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) k[u] = todo[u] ? region[sl[u]] : 0ull;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      old[u] = k[u];
-      if (todo[u] && k[u] == 0)
-        old[u] = atomicCAS(&region[sl[u]], 0ull, bit | code[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!todo[u]) continue;
-      if (old[u] == 0) {  // claimed, the bit with it
-        g[u] = (r << w.cap_log2) + sl[u];
-        todo[u] = false;
-      } else if (gt_code(old[u]) == code[u]) {  // the code's word
-        atomicOr(&region[sl[u]], bit);
-        g[u] = (r << w.cap_log2) + sl[u];
-        todo[u] = false;
-      } else {  // another code's word
-        sl[u] = (sl[u] + 1) & (w.cap - 1);
-        if (--left[u] == 0) todo[u] = false;
-      }
-      any = any || todo[u];
-    }
-    if (!any) return;
-  }
-}
-
-// The word at `code`'s home in region r (loaded apart from its use).
-__device__ __forceinline__ unsigned long long gt_first_word(const BulkWs& w, int64_t r,
-                                                           uint32_t code) {
-  return w.gt[(r << w.cap_log2) + gt_home(code, w.cap)];
-}
-
-// The word of `code` in region r of the group table, or 0; k0 is the word at its home.
+// The word of `code` (hash h) in its quarter of partition r's table, or 0.
 __device__ __forceinline__ unsigned long long gt_word(const BulkWs& w, int64_t r, uint32_t code,
-                                                     unsigned long long k0) {
-  const unsigned long long* region = w.gt + (r << w.cap_log2);
-  int32_t s = gt_home(code, w.cap);
-  unsigned long long k = k0;
-  for (int32_t left = w.cap; left > 0; --left) {
+                                                     uint64_t h) {
+  const unsigned long long* quarter =
+      w.gt + (r << w.cap_log2) + static_cast<int64_t>(gt_quarter(h)) * w.sub;
+  int32_t s = static_cast<int32_t>(h & static_cast<uint64_t>(w.sub - 1));
+  for (int32_t left = w.sub; left > 0; --left) {
+    const unsigned long long k = quarter[s];
     if (k == 0 || gt_code(k) == code) return k;
-    s = (s + 1) & (w.cap - 1);
-    k = region[s];
+    s = (s + 1) & (w.sub - 1);
   }
   return 0;
 }
@@ -676,13 +629,9 @@ __device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int
   return -1;
 }
 
-__global__ __launch_bounds__(256) void bulk_clear_kernel(BulkWs w, int64_t P) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t words = P << w.cap_log2;
-  ulonglong2* gt2 = reinterpret_cast<ulonglong2*>(w.gt);
-  for (int64_t i = i0; i < words / 2; i += stride) gt2[i] = ulonglong2{0ull, 0ull};
-  for (int64_t i = i0; i < P; i += stride) w.zero_slot[i] = -1;
+__device__ __forceinline__ int32_t chunk_find(const BulkWs& w, int64_t p, int c, uint32_t code) {
+  const int64_t sum = p * w.nch + c;
+  return summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code);
 }
 
 __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkWs w) {
@@ -733,33 +682,131 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
   }
   __syncthreads();
 
-  // 3. the summary, and every distinct code into the group table
+  // 3. the summary, and the distinct codes listed per group-table quarter (a wave takes its
+  // places in a list with one LDS atomic)
+  __shared__ int32_t n_in[kQuarters];
+  if (t < kQuarters) n_in[t] = 0;
   const int64_t sum = p * w.nch + c;
   uint32_t* scode = w.sum_code + sum * kSlots;
   int32_t* spos = w.sum_pos + sum * kSumPos;
   for (int x = t; x < kSlots; x += kThreads) scode[x] = s.code[x];
   for (int x = t; x <= kSlots; x += kThreads) spos[x] = s.pos[x];
-  constexpr int U = 4;  // codes per thread whose probes overlap
-  for (int x0 = t; x0 <= kSlots; x0 += U * kThreads) {
-    uint32_t code[U];
-    bool act[U];
+  __syncthreads();
+  const int lane = t & 63;
+  uint32_t* lists = w.qlist + sum * kQuarters * kChunk;
+  for (int x0 = 0; x0 <= kSlots; x0 += kThreads) {  // the same trip count in every thread
+    const int x = x0 + t;
+    const uint32_t code = x < kSlots ? s.code[x] : SENT;
+    const bool held = x < kSlots ? code != SENT : x == kSlots && s.pos[kSlots] >= 0;
+    const int q = held ? gt_quarter(splitmix_fin(code)) : 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int x = x0 + u * kThreads;
-      act[u] = x <= kSlots && s.pos[x] >= 0;
-      code[u] = x < kSlots ? s.code[x] : SENT;
-    }
-    int64_t g[U];
-    gt_enter<U>(w, p, code, act, c, g);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!act[u]) continue;
-      if (g[u] < 0)  // cannot happen with the region at most half full; fail loudly
-        atomicOr(a.full, 2);
-      else if (code[u] == 0)
-        w.zero_slot[p] = g[u];
+    for (int qq = 0; qq < kQuarters; ++qq) {
+      const unsigned long long b = __ballot(held && q == qq);
+      if (b == 0) continue;
+      const int leader = __ffsll(b) - 1;
+      int at = 0;
+      if (lane == leader) at = atomicAdd(&n_in[qq], static_cast<int32_t>(__popcll(b)));
+      at = __shfl(at, leader);
+      if (held && q == qq) lists[qq * kChunk + at + __popcll(b & ((1ull << lane) - 1))] = code;
     }
   }
+  __syncthreads();
+  if (t < kQuarters) w.qcount[sum * kQuarters + t] = n_in[t];
+}
+
+// Code slot x (x == kSlots: the sentinel code's own entry) of chunk c's summary: the code, and
+// whether the chunk holds keys with it.
+__device__ __forceinline__ bool summary_slot(const BulkWs& w, int64_t p, int c, int x,
+                                             uint32_t& code) {
+  const int64_t sum = p * w.nch + c;
+  if (x < kSlots) {
+    code = w.sum_code[sum * kSlots + x];
+    return code != sentinel<uint32_t>();
+  }
+  code = sentinel<uint32_t>();
+  return w.sum_pos[sum * kSumPos + kSlots] >= 0;
+}
+
+// One workgroup per (partition, quarter): the quarter's table built in LDS from the quarter's
+// code lists of every chunk of the partition, one CAS (new code) or OR (its chunk bit) per code
+// and chunk, then written out whole. With more than 3/4 of the quarter's words taken the quarter
+// is marked spilled and the table is not written (codes met after that are not entered; one
+// that finds no free word can only do so with the table past that mark).
+__global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
+  __shared__ unsigned long long tab[kQuarterMax];
+  __shared__ int32_t start[kBulkSpan / kChunk + 1];  // the quarter's codes before chunk c
+  __shared__ int32_t n_codes, zero_at;
+  const int64_t p = blockIdx.x / kQuarters;
+  const int qt = static_cast<int>(blockIdx.x % kQuarters);
+  const int t = threadIdx.x;
+  const int sub = w.sub;
+  const int limit = sub / 4 * 3;
+  for (int x = t; x < sub; x += kTableThreads) tab[x] = 0ull;
+  if (t == 0) {
+    n_codes = 0;
+    zero_at = -1;
+    int32_t run = 0;
+    for (int c = 0; c < w.nch; ++c) {
+      start[c] = run;
+      run += w.qcount[(p * w.nch + c) * kQuarters + qt];
+    }
+    start[w.nch] = run;
+  }
+  __syncthreads();
+  const int total = start[w.nch];
+  constexpr int U = 8;  // codes per thread whose loads are in flight together
+  for (int f0 = t; f0 < total; f0 += U * kTableThreads) {
+    uint32_t code[U];
+    int chunk[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int f = f0 + u * kTableThreads;
+      int lo = 0, hi = w.nch;  // the chunk c with start[c] <= f < start[c + 1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (start[mid] <= f) lo = mid; else hi = mid;
+      }
+      chunk[u] = f < total ? lo : -1;
+      code[u] = f < total ? w.qlist[((p * w.nch + lo) * kQuarters + qt) * kChunk + (f - start[lo])]
+                          : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bool entered = false;
+      if (chunk[u] >= 0 &&
+          __hip_atomic_load(&n_codes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <= limit) {
+        const unsigned long long bit = 1ull << (32 + chunk[u]);
+        int s = static_cast<int>(splitmix_fin(code[u]) & static_cast<uint64_t>(sub - 1));
+        for (int left = sub; left > 0; --left) {
+          const unsigned long long k = atomicCAS(&tab[s], 0ull, bit | code[u]);
+          if (k == 0) {  // entered
+            entered = true;
+            if (code[u] == 0) zero_at = s;
+            break;
+          }
+          if (gt_code(k) == code[u]) {
+            atomicOr(&tab[s], bit);
+            break;
+          }
+          s = (s + 1) & (sub - 1);
+        }
+      }
+      // one count update per wave, by its lowest lane still in the loop
+      const unsigned long long b = __ballot(entered);
+      if ((t & 63) == __ffsll(__ballot(true)) - 1 && b != 0)
+        atomicAdd(&n_codes, static_cast<int32_t>(__popcll(b)));
+    }
+  }
+  __syncthreads();
+  const bool spill = n_codes > limit;
+  if (t == 0) {
+    w.spilled[blockIdx.x] = spill ? 1 : 0;
+    if (gt_quarter(splitmix_fin(0)) == qt)
+      w.zero_slot[p] = !spill && zero_at >= 0 ? (p << w.cap_log2) + qt * sub + zero_at : -1;
+  }
+  if (spill) return;
+  unsigned long long* dst = w.gt + (p << w.cap_log2) + static_cast<int64_t>(qt) * sub;
+  for (int x = t; x < sub; x += kTableThreads) dst[x] = tab[x];
 }
 
 // One lane per query of the sub-call.
@@ -779,14 +826,21 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
     const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
     const int64_t h = home_slot(code, tag - 2, a.cap);
     const PairHead first = load_pair(a, h, a.cap);
-    const unsigned long long word = gt_word(w, p, code, gt_first_word(w, p, code));
+    const uint64_t gh = splitmix_fin(code);
     const int c = o / kChunk;
-    const uint32_t m = static_cast<uint32_t>(word >> 32) & ((1u << c) - 1u);
-    if (m) {
-      const int c2 = 31 - __clz(m);
-      const int64_t sum = p * w.nch + c2;
-      const int32_t lp = summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code);
-      j = lp >= 0 ? c2 * kChunk + lp : -1;
+    if (!w.spilled[p * kQuarters + gt_quarter(gh)]) {
+      const unsigned long long word = gt_word(w, p, code, gh);
+      const uint32_t m = static_cast<uint32_t>(word >> 32) & ((1u << c) - 1u);
+      if (m) {
+        const int c2 = 31 - __clz(m);
+        const int32_t lp = chunk_find(w, p, c2, code);
+        j = lp >= 0 ? c2 * kChunk + lp : -1;
+      }
+    } else {  // spilled quarter: the summaries of the earlier chunks, latest first
+      for (int c2 = c - 1; c2 >= 0 && j < 0; --c2) {
+        const int32_t lp = chunk_find(w, p, c2, code);
+        if (lp >= 0) j = c2 * kChunk + lp;
+      }
     }
     if (j < 0) {
       const int64_t sl = lane_lookup(a, code, tag, h, first);
@@ -797,23 +851,15 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
   group_copy<1>(a, dst, a.values + (base + j) * a.vbytes, 0);
 }
 
-// Word g of the group table (partition p): the value of its code's latest key in the sub-call
-// over the code's existing store entry, or into a claimed slot. The lookups of this sub-call are
-// over (previous kernel), and no other item looks for the same key, so the only thing a
-// concurrent claim can be mistaken for is code 0 (a claimed slot whose code is not written yet
-// reads as 0): code-0 keys wait for bulk_zero_kernel. Returns 1 for a claim.
-__device__ __forceinline__ int bulk_insert_word(const StoreArgs& a, const BulkWs& w, int64_t p,
-                                                unsigned long long word) {
-  const uint32_t code = gt_code(word);
-  const int c2 = 31 - __clz(static_cast<uint32_t>(word >> 32));
-  const int64_t sum = p * w.nch + c2;
-  const int32_t lp = summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code);
-  if (lp < 0) {  // the summary of a chunk in the mask holds the code; fail loudly
-    atomicOr(a.full, 2);
-    return 0;
-  }
+// The key of partition p with `code` at position lp of chunk c (its latest in the sub-call):
+// its value over the code's existing store entry, or into a claimed slot. The lookups of this
+// sub-call are over (previous kernel), and no other item looks for the same key, so the only
+// thing a concurrent claim can be mistaken for is code 0 (a claimed slot whose code is not
+// written yet reads as 0): code-0 keys wait for bulk_zero_kernel. Returns 1 for a claim.
+__device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, uint32_t code, int c,
+                                               int32_t lp) {
   const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-  const uint8_t* v = a.values + (p * a.T + a.s0 + c2 * kChunk + lp) * a.vbytes;
+  const uint8_t* v = a.values + (p * a.T + a.s0 + c * kChunk + lp) * a.vbytes;
   u32x4 vals[kSpecPieces];  // the value row, loaded with the first probe
 #pragma unroll
   for (int k = 0; k < kSpecPieces; ++k)
@@ -824,36 +870,86 @@ __device__ __forceinline__ int bulk_insert_word(const StoreArgs& a, const BulkWs
   return r > 0 ? 1 : 0;
 }
 
-// One lane per word of the group table. A workgroup's words lie in one region (regions are at
-// least 1024 words); it writes its number of claims to `claims`, and bulk_zero_kernel adds a
-// region's numbers to the partition's count once: the region's workgroups run close together in
-// time, so atomics on the partition's count would serialise.
+// A word of the group table: its code's latest key is in the highest chunk of its mask.
+__device__ __forceinline__ int bulk_insert_word(const StoreArgs& a, const BulkWs& w, int64_t p,
+                                                unsigned long long word) {
+  const uint32_t code = gt_code(word);
+  const int c2 = 31 - __clz(static_cast<uint32_t>(word >> 32));
+  const int32_t lp = chunk_find(w, p, c2, code);
+  if (lp < 0) {  // the summary of a chunk in the mask holds the code; fail loudly
+    atomicOr(a.full, 2);
+    return 0;
+  }
+  return bulk_insert_key(a, p, code, c2, lp);
+}
+
+// One lane per word of the group table; a workgroup's 256 words lie in one quarter (quarters
+// are at least 256 words). A spilled quarter's workgroups instead take the (chunk, summary
+// slot) pairs of the partition whose code falls in the quarter and insert those whose code no
+// later chunk holds. Each workgroup writes its number of claims to `claims`, and
+// bulk_zero_kernel adds a partition's numbers to its count once: a partition's workgroups run
+// close together in time, so atomics on its count would serialise.
 __global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w) {
   __shared__ uint32_t n_claims;
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t p = g >> w.cap_log2;
+  const int qt = static_cast<int>((g & (w.cap - 1)) / w.sub);
   if (threadIdx.x == 0) n_claims = 0;
   __syncthreads();
-  const unsigned long long word = w.gt[g];
   int claimed = 0;
-  if (word != 0 && gt_code(word) != 0) claimed = bulk_insert_word(a, w, g >> w.cap_log2, word);
-  const unsigned long long b = __ballot(claimed);
-  if ((threadIdx.x & 63) == 0 && b != 0) atomicAdd(&n_claims, static_cast<uint32_t>(__popcll(b)));
+  if (!w.spilled[p * kQuarters + qt]) {
+    const unsigned long long word = w.gt[g];
+    if (word != 0 && gt_code(word) != 0) claimed = bulk_insert_word(a, w, p, word);
+  } else {
+    const int per_chunk = kSlots + 1;
+    const int64_t lanes = w.sub;  // the quarter's lanes, one per word
+    for (int64_t q = (g & (w.sub - 1)); q < static_cast<int64_t>(w.nch) * per_chunk; q += lanes) {
+      const int c = static_cast<int>(q / per_chunk);
+      const int x = static_cast<int>(q - static_cast<int64_t>(c) * per_chunk);
+      uint32_t code;
+      if (!summary_slot(w, p, c, x, code) || code == 0 || gt_quarter(splitmix_fin(code)) != qt)
+        continue;
+      bool later = false;
+      for (int c2 = c + 1; c2 < w.nch && !later; ++c2) later = chunk_find(w, p, c2, code) >= 0;
+      if (later) continue;
+      const int64_t sum = p * w.nch + c;
+      claimed += bulk_insert_key(a, p, code, c, w.sum_pos[sum * kSumPos + x]);
+    }
+  }
+  const unsigned long long b = __ballot(claimed != 0);
+  uint32_t mine = claimed;
+  for (int d = 32; d > 0; d >>= 1) mine += __shfl_xor(mine, d);  // claims of the wave
+  if ((threadIdx.x & 63) == 0 && b != 0) atomicAdd(&n_claims, mine);
   __syncthreads();
   if (threadIdx.x == 0) w.claims[blockIdx.x] = n_claims;
 }
 
 // One workgroup per partition: the insert of code 0, then the partition's claims of the
-// sub-call (its region's workgroup numbers, and code 0's) added to its count.
-__global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, int32_t blocks_per_region) {
+// sub-call (its workgroup numbers, and code 0's) added to its count.
+__global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, int32_t blocks_per_part) {
   __shared__ uint32_t total;
   const int64_t p = blockIdx.x;
   const int t = threadIdx.x;
   if (t == 0) total = 0;
   __syncthreads();
-  const int64_t g = w.zero_slot[p];
-  if (t == 0 && g >= 0 && bulk_insert_word(a, w, p, w.gt[g])) atomicAdd(&total, 1u);
+  if (t == 0) {
+    int r = 0;
+    if (!w.spilled[p * kQuarters + gt_quarter(splitmix_fin(0))]) {
+      const int64_t g = w.zero_slot[p];
+      if (g >= 0) r = bulk_insert_word(a, w, p, w.gt[g]);
+    } else {  // spilled quarter: code 0's latest chunk from the summaries
+      for (int c = w.nch - 1; c >= 0; --c) {
+        const int32_t lp = chunk_find(w, p, c, 0u);
+        if (lp >= 0) {
+          r = bulk_insert_key(a, p, 0u, c, lp);
+          break;
+        }
+      }
+    }
+    if (r) atomicAdd(&total, 1u);
+  }
   uint32_t sum = 0;
-  for (int i = t; i < blocks_per_region; i += blockDim.x) sum += w.claims[p * blocks_per_region + i];
+  for (int i = t; i < blocks_per_part; i += blockDim.x) sum += w.claims[p * blocks_per_part + i];
   if (sum) atomicAdd(&total, sum);
   __syncthreads();
   if (t == 0 && total) atomicAdd(&a.counts[a.g0 + p], static_cast<unsigned long long>(total));
@@ -861,7 +957,8 @@ __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, i
 
 // Workspace layout of a bulk call of P partitions (sub-calls of S positions).
 struct BulkLayout {
-  int64_t cap, cap_log2, nch, off_zero, off_scode, off_spos, off_src, off_claims, bytes;
+  int64_t cap, cap_log2, nch, off_spill, off_zero, off_scode, off_spos, off_src, off_qlist,
+      off_qcount, off_claims, bytes;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -877,6 +974,8 @@ BulkLayout bulk_layout(int64_t P, int64_t T) {
   }
   L.nch = (S + kChunk - 1) / kChunk;
   int64_t o = align256(P * L.cap * 8);
+  L.off_spill = o;
+  o += align256(P * kQuarters * 4);
   L.off_zero = o;
   o += align256(P * 8);
   L.off_scode = o;
@@ -885,11 +984,16 @@ BulkLayout bulk_layout(int64_t P, int64_t T) {
   o += align256(P * L.nch * kSumPos * 4);
   L.off_src = o;
   o += align256(P * S * 4);
+  L.off_qlist = o;
+  o += align256(P * L.nch * kQuarters * kChunk * 4);
+  L.off_qcount = o;
+  o += align256(P * L.nch * kQuarters * 4);
   L.off_claims = o;
   o += align256(P * L.cap / 256 * 4);
   L.bytes = o;
   return L;
 }
+static_assert(2 * kBulkSpan / kQuarters <= kQuarterMax, "a quarter fits the LDS table");
 
 }  // namespace
 }  // namespace lema
@@ -911,29 +1015,33 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   BulkWs w{};
   w.gt = reinterpret_cast<unsigned long long*>(ws);
+  w.spilled = reinterpret_cast<int32_t*>(ws + L.off_spill);
   w.zero_slot = reinterpret_cast<int64_t*>(ws + L.off_zero);
   w.sum_code = reinterpret_cast<uint32_t*>(ws + L.off_scode);
   w.sum_pos = reinterpret_cast<int32_t*>(ws + L.off_spos);
   w.src_in = reinterpret_cast<int32_t*>(ws + L.off_src);
+  w.qlist = reinterpret_cast<uint32_t*>(ws + L.off_qlist);
+  w.qcount = reinterpret_cast<int32_t*>(ws + L.off_qcount);
   w.claims = reinterpret_cast<uint32_t*>(ws + L.off_claims);
   w.cap = static_cast<int32_t>(L.cap);
   w.cap_log2 = static_cast<int32_t>(L.cap_log2);
-  const int32_t blocks_per_region = static_cast<int32_t>(L.cap / 256);  // whole: cap >= 1024
+  w.sub = static_cast<int32_t>(L.cap / kQuarters);
+  const int32_t blocks_per_part = static_cast<int32_t>(L.cap / 256);  // whole: cap >= 1024
   for (int64_t s0 = 0; s0 < a.T; s0 += kBulkSpan) {
     a.s0 = s0;
     a.len = static_cast<int32_t>(a.T - s0 < kBulkSpan ? a.T - s0 : kBulkSpan);
     w.nch = (a.len + kChunk - 1) / kChunk;
-    bulk_clear_kernel<<<dim3(2048), dim3(256), 0, st>>>(w, P);
-    if (int rc = launch_status("bulk_clear_kernel")) return rc;
     bulk_chunk_kernel<<<dim3(P * w.nch), dim3(kThreads), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_chunk_kernel")) return rc;
+    bulk_table_kernel<<<dim3(P * kQuarters), dim3(kTableThreads), 0, st>>>(w);
+    if (int rc = launch_status("bulk_table_kernel")) return rc;
     if (a.qc != nullptr) {
       bulk_query_kernel<<<dim3((P * a.len + 255) / 256), dim3(256), 0, st>>>(a, w);
       if (int rc = launch_status("bulk_query_kernel")) return rc;
     }
-    bulk_insert_kernel<<<dim3(P * blocks_per_region), dim3(256), 0, st>>>(a, w);
+    bulk_insert_kernel<<<dim3(P * blocks_per_part), dim3(256), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_insert_kernel")) return rc;
-    bulk_zero_kernel<<<dim3(P), dim3(256), 0, st>>>(a, w, blocks_per_region);
+    bulk_zero_kernel<<<dim3(P), dim3(256), 0, st>>>(a, w, blocks_per_part);
     if (int rc = launch_status("bulk_zero_kernel")) return rc;
   }
   return LEMA_OK;

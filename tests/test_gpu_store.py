@@ -277,6 +277,55 @@ def test_bulk_region_at_design_load(dev):
     store.check_full()
 
 
+def _splitmix_fin(x):
+    """splitmix64's finaliser on uint64 arrays (the bulk path's group-table hash)."""
+    x = np.asarray(x, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return x ^ (x >> np.uint64(31))
+
+
+def _bulk_group_cap(T):
+    s = min(T, 32 * 1024)
+    cap = 1024
+    while cap < 2 * s:
+        cap *= 2
+    return cap
+
+
+def test_bulk_spilled_quarter(dev):
+    """Key codes chosen so that one quarter of a partition's group table gets more codes than
+    its LDS table takes (3/4 of its words): that quarter's queries and inserts search the chunk
+    summaries instead, code 0 among them. Another partition uses the same quarter with few
+    codes and a third ordinary codes; two calls, against the dict."""
+    rng = np.random.default_rng(18)
+    P, T = 3, 6000
+    cand = rng.integers(1, 1 << 31, size=200_000, dtype=np.int64)
+    q0 = cand[(_splitmix_fin(cand) >> np.uint64(62)) == 0]           # codes of quarter 0
+    assert int(_splitmix_fin(0) >> np.uint64(62)) == 0               # code 0 is one of them
+    pools = [np.concatenate([[0], q0[:5500]]), q0[5500:6000], cand[:3000]]
+    limit = _bulk_group_cap(T) // 4 // 4 * 3
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=200_000, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    for call in range(2):
+        kc = np.concatenate([rng.choice(pool, size=T) for pool in pools])
+        assert len(set(kc[:T].tolist())) > limit and len(set(kc[T:2 * T].tolist())) < limit
+        qc = np.concatenate([rng.choice(pool, size=T) for pool in pools])
+        miss = rng.random(P * T) < 0.2
+        qc[miss] = rng.integers(1 << 30, 1 << 31, size=int(miss.sum()))
+        vals = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+        out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev).to(torch.int32),
+                       torch.from_numpy(kc).to(dev).to(torch.int32),
+                       torch.from_numpy(vals.view(np.int16)).to(dev), out, T, 0)
+        want = ref.exchange(qc, kc, vals.view(np.uint8).reshape(-1, 2 * D_V), T, 0)
+        got = out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V)
+        assert np.array_equal(got, want), call
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    store.check_full()
+
+
 @pytest.mark.parametrize("d_v", [32, 40, 64])
 def test_bulk_long_value_rows(dev, d_v):
     """Rows of 64, 80 and 128 bytes through two long calls: up to four 16-byte pieces a key's
