@@ -120,7 +120,7 @@ int64_t lema_store_workspace_bytes(int64_t n, int64_t T, int32_t code_bytes);
 
 /* lema_store_exchange with a device workspace (256-byte aligned, at least
  * lema_store_workspace_bytes): a call with 32-bit codes and T > 2048 then runs in sub-calls of
- * up to 65536 positions, each as a few kernels over all of its items (in-chunk resolution,
+ * up to 32768 positions, each as a few kernels over all of its items (in-chunk resolution,
  * per-chunk key summaries and a scratch table of every (partition, code) of the sub-call),
  * instead of one launch per 1024 positions. Same results as lema_store_exchange
  * (code/lema/csrc/store.cpp:122-162). workspace NULL = lema_store_exchange. */

@@ -566,6 +566,8 @@ constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots,
 constexpr int kQuarters = 4;            // group-table quarters per partition
 constexpr int kQuarterMax = 16384;      // words of a quarter: the LDS table (128 KB)
 constexpr int kTableThreads = 1024;
+constexpr int kFilterBitsLog2 = 16;     // key-code filter bits per quarter (8 KB)
+constexpr int kFilterWordsQ = (1 << kFilterBitsLog2) / 32;
 
 // Group table: per partition `cap` 64-bit words, kQuarters quarters of `sub` words; a code
 // lives in the quarter given by the top bits of its hash, at the slot given by the low bits,
@@ -583,6 +585,8 @@ struct BulkWs {
                            // of the quarter, up to kChunk
   int32_t* qcount;         // per (partition, chunk, quarter): their number
   uint32_t* claims;        // per workgroup of bulk_insert_kernel: store slots it claimed
+  uint32_t* filter;        // per (partition, quarter): kFilterWordsQ words, two bits set per
+                           // key code of the sub-call (gt_filter_bits)
   int32_t cap;             // words per partition: a power of two, at least twice kBulkSpan
   int32_t cap_log2;
   int32_t sub;             // words per quarter: cap / kQuarters
@@ -590,6 +594,14 @@ struct BulkWs {
 };
 
 __device__ __forceinline__ int gt_quarter(uint64_t h) { return static_cast<int>(h >> 62); }
+
+// A code's two bits in its quarter's key-code filter: hash bits that neither the quarter (the
+// top two) nor the slot (at most the low 14) uses.
+__device__ __forceinline__ void gt_filter_bits(uint64_t h, uint32_t& b1, uint32_t& b2) {
+  constexpr uint64_t m = (1u << kFilterBitsLog2) - 1;
+  b1 = static_cast<uint32_t>((h >> 20) & m);
+  b2 = static_cast<uint32_t>((h >> (20 + kFilterBitsLog2)) & m);
+}
 
 __device__ __forceinline__ uint32_t gt_code(unsigned long long word) {
   return static_cast<uint32_t>(word);
@@ -734,6 +746,7 @@ __device__ __forceinline__ bool summary_slot(const BulkWs& w, int64_t p, int c, 
 // that finds no free word can only do so with the table past that mark).
 __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   __shared__ unsigned long long tab[kQuarterMax];
+  __shared__ uint32_t bits[kFilterWordsQ];
   __shared__ int32_t start[kBulkSpan / kChunk + 1];  // the quarter's codes before chunk c
   __shared__ int32_t n_codes, zero_at;
   const int64_t p = blockIdx.x / kQuarters;
@@ -742,6 +755,7 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   const int sub = w.sub;
   const int limit = sub / 4 * 3;
   for (int x = t; x < sub; x += kTableThreads) tab[x] = 0ull;
+  for (int x = t; x < kFilterWordsQ; x += kTableThreads) bits[x] = 0u;
   if (t == 0) {
     n_codes = 0;
     zero_at = -1;
@@ -773,10 +787,17 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       bool entered = false;
+      const uint64_t h = splitmix_fin(code[u]);
+      if (chunk[u] >= 0) {  // every code of the quarter, spilled or not, sets its filter bits
+        uint32_t b1, b2;
+        gt_filter_bits(h, b1, b2);
+        atomicOr(&bits[b1 >> 5], 1u << (b1 & 31));
+        atomicOr(&bits[b2 >> 5], 1u << (b2 & 31));
+      }
       if (chunk[u] >= 0 &&
           __hip_atomic_load(&n_codes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <= limit) {
         const unsigned long long bit = 1ull << (32 + chunk[u]);
-        int s = static_cast<int>(splitmix_fin(code[u]) & static_cast<uint64_t>(sub - 1));
+        int s = static_cast<int>(h & static_cast<uint64_t>(sub - 1));
         for (int left = sub; left > 0; --left) {
           const unsigned long long k = atomicCAS(&tab[s], 0ull, bit | code[u]);
           if (k == 0) {  // entered
@@ -804,6 +825,8 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
     if (gt_quarter(splitmix_fin(0)) == qt)
       w.zero_slot[p] = !spill && zero_at >= 0 ? (p << w.cap_log2) + qt * sub + zero_at : -1;
   }
+  uint32_t* fdst = w.filter + static_cast<int64_t>(blockIdx.x) * kFilterWordsQ;
+  for (int x = t; x < kFilterWordsQ; x += kTableThreads) fdst[x] = bits[x];
   if (spill) return;
   unsigned long long* dst = w.gt + (p << w.cap_log2) + static_cast<int64_t>(qt) * sub;
   for (int x = t; x < sub; x += kTableThreads) dst[x] = tab[x];
@@ -828,7 +851,13 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
     const PairHead first = load_pair(a, h, a.cap);
     const uint64_t gh = splitmix_fin(code);
     const int c = o / kChunk;
-    if (!w.spilled[p * kQuarters + gt_quarter(gh)]) {
+    const int64_t pq = p * kQuarters + gt_quarter(gh);
+    uint32_t b1, b2;
+    gt_filter_bits(gh, b1, b2);
+    const uint32_t* f = w.filter + pq * kFilterWordsQ;
+    if (!((f[b1 >> 5] >> (b1 & 31)) & (f[b2 >> 5] >> (b2 & 31)) & 1u)) {
+      // no key of the sub-call has this code (no false negatives): the store
+    } else if (!w.spilled[pq]) {
       const unsigned long long word = gt_word(w, p, code, gh);
       const uint32_t m = static_cast<uint32_t>(word >> 32) & ((1u << c) - 1u);
       if (m) {
@@ -958,7 +987,7 @@ __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, i
 // Workspace layout of a bulk call of P partitions (sub-calls of S positions).
 struct BulkLayout {
   int64_t cap, cap_log2, nch, off_spill, off_zero, off_scode, off_spos, off_src, off_qlist,
-      off_qcount, off_claims, bytes;
+      off_qcount, off_claims, off_filter, bytes;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -990,6 +1019,8 @@ BulkLayout bulk_layout(int64_t P, int64_t T) {
   o += align256(P * L.nch * kQuarters * 4);
   L.off_claims = o;
   o += align256(P * L.cap / 256 * 4);
+  L.off_filter = o;
+  o += align256(P * kQuarters * kFilterWordsQ * 4);
   L.bytes = o;
   return L;
 }
@@ -1023,6 +1054,7 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
   w.qlist = reinterpret_cast<uint32_t*>(ws + L.off_qlist);
   w.qcount = reinterpret_cast<int32_t*>(ws + L.off_qcount);
   w.claims = reinterpret_cast<uint32_t*>(ws + L.off_claims);
+  w.filter = reinterpret_cast<uint32_t*>(ws + L.off_filter);
   w.cap = static_cast<int32_t>(L.cap);
   w.cap_log2 = static_cast<int32_t>(L.cap_log2);
   w.sub = static_cast<int32_t>(L.cap / kQuarters);
