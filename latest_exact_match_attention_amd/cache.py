@@ -88,8 +88,8 @@ class HashStore:
         position order. Device tensors: codes int64 (or int32 for codes below 2^32), values and
         out rows of `vbytes` bytes in any dtype. `qcodes=None` only inserts. With `check` the
         full flag is read back (a device sync) and a full table raises like the reference;
-        without it, call `check_full()` later (e.g. after a graph replay). A long call (int32
-        codes, T > 2048) takes the bulk path with a device workspace this store keeps."""
+        without it, call `check_full()` later (e.g. after a graph replay). A long call
+        (T > 2048) takes the bulk path with a device workspace this store keeps."""
         kc, cb = _codes(kcodes)
         n = kc.numel()
         if qcodes is not None:

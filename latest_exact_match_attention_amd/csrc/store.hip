@@ -541,15 +541,15 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, cons
 }
 
 // ------------------------------------------------------------------ bulk calls
-// A call with many positions per partition (32-bit codes) runs in sub-calls of up to kBulkSpan
-// positions, each as a few kernels over all of its items at once instead of one launch per
-// 1024-position sub-chunk:
+// A call with many positions per partition runs in sub-calls of up to kBulkSpan positions, each
+// as a few kernels over all of its items at once instead of one launch per 1024-position
+// sub-chunk:
 //   chunks   one workgroup per (partition, 1024-chunk): in-chunk answers of the queries (LDS
-//            resolver) and the chunk's key summary (code -> latest position, the LDS table
-//            written out);
-//   table    one workgroup per (partition, quarter of the code hash space): the quarter's codes
-//            of every chunk summary entered in an LDS table, code -> mask of the chunks holding
-//            keys with it, written out as that quarter of the partition's group table;
+//            resolver), the chunk's key summary (code -> latest position, the LDS table
+//            written out), and its distinct key codes listed per part of the group table;
+//   table    one workgroup per (partition, part of the code hash space): the part's codes of
+//            every chunk entered in an LDS table, code -> mask of the chunks holding keys with
+//            it, written out as that part of the partition's group table;
 //   queries  a query without an in-chunk answer takes the highest chunk below its own in its
 //            code's mask and that chunk's summary gives the key; with no such chunk it looks
 //            the store up (the table still holds exactly the keys before the sub-call);
@@ -557,46 +557,67 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, cons
 //            the highest chunk in its mask and writes that value over its existing store entry
 //            or claims a slot (code 0 in a kernel of its own, see bulk_insert_kernel); the
 //            claims are counted per partition on the way.
-// The kernel boundary orders every lookup of the sub-call before its inserts. A quarter with
+// The kernel boundary orders every lookup of the sub-call before its inserts. A part with
 // more codes than its LDS table takes (only codes chosen to collide in the hash get there) is
 // marked spilled: its queries and inserts then search the chunk summaries themselves.
 constexpr int kBulkSpan = 32 * kChunk;  // positions per sub-call: chunk masks fit 32 bits
 static_assert((kSlots & (kSlots - 1)) == 0, "chunk summaries are probed with a slot mask");
 constexpr int kSumPos = kSlots + 4;     // summary positions: kSlots code slots, the sentinel's
-constexpr int kQuarters = 4;            // group-table quarters per partition
-constexpr int kQuarterMax = 16384;      // words of a quarter: the LDS table (128 KB)
 constexpr int kTableThreads = 1024;
-constexpr int kFilterBitsLog2 = 16;     // key-code filter bits per quarter (8 KB)
+constexpr int kTableLdsBytes = 131072;  // the table kernel's LDS table
+constexpr int kFilterBitsLog2 = 16;     // key-code filter bits per part (8 KB)
 constexpr int kFilterWordsQ = (1 << kFilterBitsLog2) / 32;
 
-// Group table: per partition `cap` 64-bit words, kQuarters quarters of `sub` words; a code
-// lives in the quarter given by the top bits of its hash, at the slot given by the low bits,
-// with linear probing inside the quarter. A word is code | mask << 32 (bit c of the mask: chunk
-// c of the sub-call holds keys with this code) or 0 for a free word; an entered word always has
-// a mask bit set.
+// Group table per partition: `cap` entries in kParts parts of `sub` entries; a code lives in the
+// part given by the top bits of its hash, at the slot given by the low bits, with linear
+// probing inside the part. Bit c of an entry's mask: chunk c of the sub-call holds keys with
+// the code.
+//   32-bit codes: 4 parts of up to 16,384 words; a word is code | mask << 32, 0 = free (an
+//     entered word always has a mask bit set).
+//   64-bit codes: 8 parts of up to 8,192 entries; an entry is a code word (the all-ones code
+//     marks a free one) and a 32-bit mask word; the all-ones code's own mask is kept per
+//     (partition, part).
+template <typename CodeT>
+struct GtTraits;
+template <>
+struct GtTraits<uint32_t> {
+  static constexpr int kParts = 4, kPartLog2 = 2, kPartMax = 16384;
+};
+template <>
+struct GtTraits<uint64_t> {
+  static constexpr int kParts = 8, kPartLog2 = 3, kPartMax = 8192;
+};
+static_assert(GtTraits<uint32_t>::kPartMax * 8 <= kTableLdsBytes, "LDS table");
+static_assert(GtTraits<uint64_t>::kPartMax * 12 <= kTableLdsBytes, "LDS table");
+
 struct BulkWs {
-  unsigned long long* gt;  // P x cap words
-  int32_t* spilled;        // per (partition, quarter): 1 = the quarter's table was not built
-  int64_t* zero_slot;      // per partition: word of code 0, or -1
-  uint32_t* sum_code;      // per (partition, chunk): the kSlots key-code slots
+  unsigned long long* gt;  // P x cap words: code | mask (32-bit codes) or codes (64-bit)
+  uint32_t* gmask;         // 64-bit codes: P x cap masks
+  uint32_t* smask;         // 64-bit codes: per (partition, part) the all-ones code's mask
+  int32_t* spilled;        // per (partition, part): 1 = the part's table was not built
+  int64_t* zero_slot;      // per partition: entry of code 0, or -1
+  void* sum_code;          // per (partition, chunk): the kSlots key-code slots
   int32_t* sum_pos;        // per (partition, chunk): kSumPos latest positions
   int32_t* src_in;         // per query of the sub-call: in-chunk answer (sub-call position) or -1
-  uint32_t* qlist;         // per (partition, chunk, quarter): the chunk's distinct key codes
-                           // of the quarter, up to kChunk
-  int32_t* qcount;         // per (partition, chunk, quarter): their number
+  void* qlist;             // per (partition, chunk, part): the chunk's distinct key codes of
+                           // the part, up to kChunk
+  int32_t* qcount;         // per (partition, chunk, part): their number
   uint32_t* claims;        // per workgroup of bulk_insert_kernel: store slots it claimed
-  uint32_t* filter;        // per (partition, quarter): kFilterWordsQ words, two bits set per
-                           // key code of the sub-call (gt_filter_bits)
-  int32_t cap;             // words per partition: a power of two, at least twice kBulkSpan
-  int32_t cap_log2;
-  int32_t sub;             // words per quarter: cap / kQuarters
+  uint32_t* filter;        // per (partition, part): kFilterWordsQ words, two bits set per key
+                           // code of the sub-call (gt_filter_bits)
+  int32_t cap;             // entries per partition: a power of two, >= 2 * kBulkSpan or less
+  int32_t cap_log2;        // for short calls, >= 256 * kParts
+  int32_t sub;             // entries per part: cap / kParts
   int32_t nch;             // chunks per partition in the sub-call
 };
 
-__device__ __forceinline__ int gt_quarter(uint64_t h) { return static_cast<int>(h >> 62); }
+template <typename CodeT>
+__device__ __forceinline__ int gt_part(uint64_t h) {
+  return static_cast<int>(h >> (64 - GtTraits<CodeT>::kPartLog2));
+}
 
-// A code's two bits in its quarter's key-code filter: hash bits that neither the quarter (the
-// top two) nor the slot (at most the low 14) uses.
+// A code's two bits in its part's key-code filter: hash bits that neither the part (at most
+// the top three) nor the slot (at most the low 14) uses.
 __device__ __forceinline__ void gt_filter_bits(uint64_t h, uint32_t& b1, uint32_t& b2) {
   constexpr uint64_t m = (1u << kFilterBitsLog2) - 1;
   b1 = static_cast<uint32_t>((h >> 20) & m);
@@ -607,30 +628,52 @@ __device__ __forceinline__ uint32_t gt_code(unsigned long long word) {
   return static_cast<uint32_t>(word);
 }
 
-// The word of `code` (hash h) in its quarter of partition r's table, or 0.
-__device__ __forceinline__ unsigned long long gt_word(const BulkWs& w, int64_t r, uint32_t code,
-                                                     uint64_t h) {
-  const unsigned long long* quarter =
-      w.gt + (r << w.cap_log2) + static_cast<int64_t>(gt_quarter(h)) * w.sub;
+// The chunk mask of `code` (hash h) in partition r's table, 0 when absent.
+template <typename CodeT>
+__device__ __forceinline__ uint32_t gt_mask_of(const BulkWs& w, int64_t r, CodeT code, uint64_t h) {
+  const int part = gt_part<CodeT>(h);
+  const int64_t base = (r << w.cap_log2) + static_cast<int64_t>(part) * w.sub;
   int32_t s = static_cast<int32_t>(h & static_cast<uint64_t>(w.sub - 1));
-  for (int32_t left = w.sub; left > 0; --left) {
-    const unsigned long long k = quarter[s];
-    if (k == 0 || gt_code(k) == code) return k;
-    s = (s + 1) & (w.sub - 1);
+  if constexpr (sizeof(CodeT) == 4) {
+    for (int32_t left = w.sub; left > 0; --left) {
+      const unsigned long long k = w.gt[base + s];
+      if (k == 0) return 0u;
+      if (gt_code(k) == code) return static_cast<uint32_t>(k >> 32);
+      s = (s + 1) & (w.sub - 1);
+    }
+  } else {
+    if (code == sentinel<CodeT>()) return w.smask[r * GtTraits<CodeT>::kParts + part];
+    for (int32_t left = w.sub; left > 0; --left) {
+      const unsigned long long k = w.gt[base + s];
+      if (k == code) return w.gmask[base + s];
+      if (k == sentinel<CodeT>()) return 0u;
+      s = (s + 1) & (w.sub - 1);
+    }
   }
-  return 0;
+  return 0u;
 }
 
 // Latest position of `code` in a chunk summary, or -1: the image of the chunk's LDS table
-// (4-slot buckets from bucket_of, linear probing), read a bucket (16 bytes) at a time; the
-// code's slot comes before any free slot on its probe path.
-__device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int32_t* pos,
-                                                uint32_t code) {
-  const uint32_t SENT = sentinel<uint32_t>();
+// (4-slot buckets from bucket_of, linear probing), read a bucket at a time; the code's slot
+// comes before any free slot on its probe path.
+template <typename CodeT>
+__device__ __forceinline__ int32_t summary_find(const CodeT* codes, const int32_t* pos, CodeT code) {
+  const CodeT SENT = sentinel<CodeT>();
   if (code == SENT) return pos[kSlots];
   int b = bucket_of<kBuckets>(fold(code));
   for (int left = kBuckets; left > 0; --left) {
-    const u32x4 e = *reinterpret_cast<const u32x4*>(codes + 4 * b);
+    CodeT e[4];
+    if constexpr (sizeof(CodeT) == 4) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(codes + 4 * b);
+      e[0] = v.x; e[1] = v.y; e[2] = v.z; e[3] = v.w;
+    } else {
+      const u32x4 v0 = *reinterpret_cast<const u32x4*>(codes + 4 * b);
+      const u32x4 v1 = *reinterpret_cast<const u32x4*>(codes + 4 * b + 2);
+      e[0] = (static_cast<uint64_t>(v0.y) << 32) | v0.x;
+      e[1] = (static_cast<uint64_t>(v0.w) << 32) | v0.z;
+      e[2] = (static_cast<uint64_t>(v1.y) << 32) | v1.x;
+      e[3] = (static_cast<uint64_t>(v1.w) << 32) | v1.z;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (e[i] == code) return pos[4 * b + i];
@@ -641,21 +684,26 @@ __device__ __forceinline__ int32_t summary_find(const uint32_t* codes, const int
   return -1;
 }
 
-__device__ __forceinline__ int32_t chunk_find(const BulkWs& w, int64_t p, int c, uint32_t code) {
+template <typename CodeT>
+__device__ __forceinline__ int32_t chunk_find(const BulkWs& w, int64_t p, int c, CodeT code) {
   const int64_t sum = p * w.nch + c;
-  return summary_find(w.sum_code + sum * kSlots, w.sum_pos + sum * kSumPos, code);
+  return summary_find<CodeT>(static_cast<const CodeT*>(w.sum_code) + sum * kSlots,
+                             w.sum_pos + sum * kSumPos, code);
 }
 
+template <typename CodeT>
 __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkWs w) {
-  __shared__ ResolveLds<uint32_t> s;
+  constexpr int kParts = GtTraits<CodeT>::kParts;
+  __shared__ ResolveLds<CodeT> s;
+  __shared__ int32_t n_in[kParts];
   const int64_t p = blockIdx.x / w.nch;
   const int c = static_cast<int>(blockIdx.x - p * w.nch);
   const int t = threadIdx.x;
   const int64_t first = p * a.T + a.s0 + static_cast<int64_t>(c) * kChunk;
   const int n = a.len - c * kChunk < kChunk ? a.len - c * kChunk : kChunk;
-  const uint32_t SENT = sentinel<uint32_t>();
-  const uint32_t* qc = static_cast<const uint32_t*>(a.qc);
-  const uint32_t* kc = static_cast<const uint32_t*>(a.kc);
+  const CodeT SENT = sentinel<CodeT>();
+  const CodeT* qc = static_cast<const CodeT*>(a.qc);
+  const CodeT* kc = static_cast<const CodeT*>(a.kc);
 
   // 1. in-chunk answers of the queries, as positions of the sub-call
   if (qc != nullptr) {
@@ -679,40 +727,38 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
   // 2. the chunk's key codes with their latest position
   for (int x = t; x < kSlots; x += kThreads) s.code[x] = SENT;
   for (int x = t; x <= kSlots; x += kThreads) s.pos[x] = -1;
+  if (t < kParts) n_in[t] = 0;
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int o = q * kThreads + t;
     if (o >= n) continue;
-    const uint32_t code = kc[first + o];
+    const CodeT code = kc[first + o];
     int slot = kSlots;
     if (code != SENT) {
       bool ins;
-      slot = table_claim<uint32_t, kBuckets>(s.code, code, SENT, bucket_of<kBuckets>(fold(code)), ins);
+      slot = table_claim<CodeT, kBuckets>(s.code, code, SENT, bucket_of<kBuckets>(fold(code)), ins);
     }
     atomicMax(&s.pos[slot], o);
   }
   __syncthreads();
 
-  // 3. the summary, and the distinct codes listed per group-table quarter (a wave takes its
+  // 3. the summary, and the distinct codes listed per group-table part (a wave takes its
   // places in a list with one LDS atomic)
-  __shared__ int32_t n_in[kQuarters];
-  if (t < kQuarters) n_in[t] = 0;
   const int64_t sum = p * w.nch + c;
-  uint32_t* scode = w.sum_code + sum * kSlots;
+  CodeT* scode = static_cast<CodeT*>(w.sum_code) + sum * kSlots;
   int32_t* spos = w.sum_pos + sum * kSumPos;
   for (int x = t; x < kSlots; x += kThreads) scode[x] = s.code[x];
   for (int x = t; x <= kSlots; x += kThreads) spos[x] = s.pos[x];
-  __syncthreads();
   const int lane = t & 63;
-  uint32_t* lists = w.qlist + sum * kQuarters * kChunk;
+  CodeT* lists = static_cast<CodeT*>(w.qlist) + sum * kParts * kChunk;
   for (int x0 = 0; x0 <= kSlots; x0 += kThreads) {  // the same trip count in every thread
     const int x = x0 + t;
-    const uint32_t code = x < kSlots ? s.code[x] : SENT;
+    const CodeT code = x < kSlots ? s.code[x] : SENT;
     const bool held = x < kSlots ? code != SENT : x == kSlots && s.pos[kSlots] >= 0;
-    const int q = held ? gt_quarter(splitmix_fin(code)) : 0;
+    const int q = held ? gt_part<CodeT>(splitmix_fin(code)) : 0;
 #pragma unroll
-    for (int qq = 0; qq < kQuarters; ++qq) {
+    for (int qq = 0; qq < kParts; ++qq) {
       const unsigned long long b = __ballot(held && q == qq);
       if (b == 0) continue;
       const int leader = __ffsll(b) - 1;
@@ -723,54 +769,70 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
     }
   }
   __syncthreads();
-  if (t < kQuarters) w.qcount[sum * kQuarters + t] = n_in[t];
+  if (t < kParts) w.qcount[sum * kParts + t] = n_in[t];
 }
 
 // Code slot x (x == kSlots: the sentinel code's own entry) of chunk c's summary: the code, and
 // whether the chunk holds keys with it.
-__device__ __forceinline__ bool summary_slot(const BulkWs& w, int64_t p, int c, int x,
-                                             uint32_t& code) {
+template <typename CodeT>
+__device__ __forceinline__ bool summary_slot(const BulkWs& w, int64_t p, int c, int x, CodeT& code) {
   const int64_t sum = p * w.nch + c;
   if (x < kSlots) {
-    code = w.sum_code[sum * kSlots + x];
-    return code != sentinel<uint32_t>();
+    code = static_cast<const CodeT*>(w.sum_code)[sum * kSlots + x];
+    return code != sentinel<CodeT>();
   }
-  code = sentinel<uint32_t>();
+  code = sentinel<CodeT>();
   return w.sum_pos[sum * kSumPos + kSlots] >= 0;
 }
 
-// One workgroup per (partition, quarter): the quarter's table built in LDS from the quarter's
-// code lists of every chunk of the partition, one CAS (new code) or OR (its chunk bit) per code
-// and chunk, then written out whole. With more than 3/4 of the quarter's words taken the quarter
-// is marked spilled and the table is not written (codes met after that are not entered; one
-// that finds no free word can only do so with the table past that mark).
+// One workgroup per (partition, part): the part's table built in LDS from the part's code
+// lists of every chunk of the partition, one CAS (new code) or OR (its chunk bit) per code and
+// chunk, then written out whole. With more than 3/4 of the part's entries taken the part is
+// marked spilled and the table is not written (codes met after that are not entered; one that
+// finds no free entry can only do so with the table past that mark).
+template <typename CodeT>
 __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
-  __shared__ unsigned long long tab[kQuarterMax];
+  constexpr int kParts = GtTraits<CodeT>::kParts;
+  constexpr bool k32 = sizeof(CodeT) == 4;
+  __shared__ __align__(16) unsigned char lds[kTableLdsBytes];
   __shared__ uint32_t bits[kFilterWordsQ];
-  __shared__ int32_t start[kBulkSpan / kChunk + 1];  // the quarter's codes before chunk c
+  __shared__ int32_t start[kBulkSpan / kChunk + 1];  // the part's codes before chunk c
   __shared__ int32_t n_codes, zero_at;
-  const int64_t p = blockIdx.x / kQuarters;
-  const int qt = static_cast<int>(blockIdx.x % kQuarters);
+  __shared__ uint32_t sent_mask;
+  unsigned long long* tab = reinterpret_cast<unsigned long long*>(lds);  // words or codes
+  uint32_t* masks = reinterpret_cast<uint32_t*>(lds + GtTraits<uint64_t>::kPartMax * 8);
+  const CodeT SENT = sentinel<CodeT>();
+  const int64_t p = blockIdx.x / kParts;
+  const int qt = static_cast<int>(blockIdx.x % kParts);
   const int t = threadIdx.x;
   const int sub = w.sub;
   const int limit = sub / 4 * 3;
-  for (int x = t; x < sub; x += kTableThreads) tab[x] = 0ull;
+  for (int x = t; x < sub; x += kTableThreads) {
+    if constexpr (k32) {
+      tab[x] = 0ull;
+    } else {
+      tab[x] = SENT;
+      masks[x] = 0u;
+    }
+  }
   for (int x = t; x < kFilterWordsQ; x += kTableThreads) bits[x] = 0u;
   if (t == 0) {
     n_codes = 0;
     zero_at = -1;
+    sent_mask = 0u;
     int32_t run = 0;
     for (int c = 0; c < w.nch; ++c) {
       start[c] = run;
-      run += w.qcount[(p * w.nch + c) * kQuarters + qt];
+      run += w.qcount[(p * w.nch + c) * kParts + qt];
     }
     start[w.nch] = run;
   }
   __syncthreads();
   const int total = start[w.nch];
+  const CodeT* qlist = static_cast<const CodeT*>(w.qlist);
   constexpr int U = 8;  // codes per thread whose loads are in flight together
   for (int f0 = t; f0 < total; f0 += U * kTableThreads) {
-    uint32_t code[U];
+    CodeT code[U];
     int chunk[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -781,14 +843,14 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
         if (start[mid] <= f) lo = mid; else hi = mid;
       }
       chunk[u] = f < total ? lo : -1;
-      code[u] = f < total ? w.qlist[((p * w.nch + lo) * kQuarters + qt) * kChunk + (f - start[lo])]
-                          : 0u;
+      code[u] = f < total ? qlist[((p * w.nch + lo) * kParts + qt) * kChunk + (f - start[lo])]
+                          : CodeT(0);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       bool entered = false;
       const uint64_t h = splitmix_fin(code[u]);
-      if (chunk[u] >= 0) {  // every code of the quarter, spilled or not, sets its filter bits
+      if (chunk[u] >= 0) {  // every code of the part, spilled or not, sets its filter bits
         uint32_t b1, b2;
         gt_filter_bits(h, b1, b2);
         atomicOr(&bits[b1 >> 5], 1u << (b1 & 31));
@@ -796,20 +858,40 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
       }
       if (chunk[u] >= 0 &&
           __hip_atomic_load(&n_codes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <= limit) {
-        const unsigned long long bit = 1ull << (32 + chunk[u]);
         int s = static_cast<int>(h & static_cast<uint64_t>(sub - 1));
-        for (int left = sub; left > 0; --left) {
-          const unsigned long long k = atomicCAS(&tab[s], 0ull, bit | code[u]);
-          if (k == 0) {  // entered
-            entered = true;
-            if (code[u] == 0) zero_at = s;
-            break;
+        if constexpr (k32) {
+          const unsigned long long bit = 1ull << (32 + chunk[u]);
+          for (int left = sub; left > 0; --left) {
+            const unsigned long long k = atomicCAS(&tab[s], 0ull, bit | code[u]);
+            if (k == 0) {  // entered
+              entered = true;
+              if (code[u] == 0) zero_at = s;
+              break;
+            }
+            if (gt_code(k) == code[u]) {
+              atomicOr(&tab[s], bit);
+              break;
+            }
+            s = (s + 1) & (sub - 1);
           }
-          if (gt_code(k) == code[u]) {
-            atomicOr(&tab[s], bit);
-            break;
+        } else {
+          const uint32_t bit = 1u << chunk[u];
+          if (code[u] == SENT) {
+            atomicOr(&sent_mask, bit);  // kept apart, takes no entry
+          } else {
+            for (int left = sub; left > 0; --left) {
+              const unsigned long long k =
+                  atomicCAS(&tab[s], static_cast<unsigned long long>(SENT),
+                            static_cast<unsigned long long>(code[u]));
+              if (k == SENT || k == code[u]) {  // entered, or the code's entry
+                atomicOr(&masks[s], bit);
+                entered = k == SENT;
+                if (entered && code[u] == 0) zero_at = s;
+                break;
+              }
+              s = (s + 1) & (sub - 1);
+            }
           }
-          s = (s + 1) & (sub - 1);
         }
       }
       // one count update per wave, by its lowest lane still in the loop
@@ -820,20 +902,26 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   }
   __syncthreads();
   const bool spill = n_codes > limit;
+  const int64_t base = (p << w.cap_log2) + static_cast<int64_t>(qt) * sub;
   if (t == 0) {
     w.spilled[blockIdx.x] = spill ? 1 : 0;
-    if (gt_quarter(splitmix_fin(0)) == qt)
-      w.zero_slot[p] = !spill && zero_at >= 0 ? (p << w.cap_log2) + qt * sub + zero_at : -1;
+    if constexpr (!k32) w.smask[blockIdx.x] = sent_mask;
+    if (gt_part<CodeT>(splitmix_fin(CodeT(0))) == qt)
+      w.zero_slot[p] = !spill && zero_at >= 0 ? base + zero_at : -1;
   }
   uint32_t* fdst = w.filter + static_cast<int64_t>(blockIdx.x) * kFilterWordsQ;
   for (int x = t; x < kFilterWordsQ; x += kTableThreads) fdst[x] = bits[x];
   if (spill) return;
-  unsigned long long* dst = w.gt + (p << w.cap_log2) + static_cast<int64_t>(qt) * sub;
-  for (int x = t; x < sub; x += kTableThreads) dst[x] = tab[x];
+  for (int x = t; x < sub; x += kTableThreads) {
+    w.gt[base + x] = tab[x];
+    if constexpr (!k32) w.gmask[base + x] = masks[x];
+  }
 }
 
 // One lane per query of the sub-call.
+template <typename CodeT>
 __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) {
+  constexpr int kParts = GtTraits<CodeT>::kParts;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t n = static_cast<int64_t>(a.n / a.T) * a.len;
   if (i >= n) return;  // partition i / len, position i % len
@@ -842,32 +930,31 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
   const int64_t base = p * a.T + a.s0;  // item of the sub-call's position 0
   uint8_t* dst = a.out + (base + o) * a.vbytes;
   int32_t j = w.src_in[i];
-  const uint32_t code = static_cast<const uint32_t*>(a.qc)[base + o];
+  const CodeT code = static_cast<const CodeT*>(a.qc)[base + o];
   if (j < 0) {
-    // the group table's and the store's first reads are in flight together: most queries
+    // the store's first read is in flight while the group table is consulted: most queries
     // without an in-chunk answer end in the store
     const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
     const int64_t h = home_slot(code, tag - 2, a.cap);
     const PairHead first = load_pair(a, h, a.cap);
     const uint64_t gh = splitmix_fin(code);
     const int c = o / kChunk;
-    const int64_t pq = p * kQuarters + gt_quarter(gh);
+    const int64_t pq = p * kParts + gt_part<CodeT>(gh);
     uint32_t b1, b2;
     gt_filter_bits(gh, b1, b2);
     const uint32_t* f = w.filter + pq * kFilterWordsQ;
     if (!((f[b1 >> 5] >> (b1 & 31)) & (f[b2 >> 5] >> (b2 & 31)) & 1u)) {
       // no key of the sub-call has this code (no false negatives): the store
     } else if (!w.spilled[pq]) {
-      const unsigned long long word = gt_word(w, p, code, gh);
-      const uint32_t m = static_cast<uint32_t>(word >> 32) & ((1u << c) - 1u);
+      const uint32_t m = gt_mask_of<CodeT>(w, p, code, gh) & ((1u << c) - 1u);
       if (m) {
         const int c2 = 31 - __clz(m);
-        const int32_t lp = chunk_find(w, p, c2, code);
+        const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
         j = lp >= 0 ? c2 * kChunk + lp : -1;
       }
-    } else {  // spilled quarter: the summaries of the earlier chunks, latest first
+    } else {  // spilled part: the summaries of the earlier chunks, latest first
       for (int c2 = c - 1; c2 >= 0 && j < 0; --c2) {
-        const int32_t lp = chunk_find(w, p, c2, code);
+        const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
         if (lp >= 0) j = c2 * kChunk + lp;
       }
     }
@@ -885,7 +972,7 @@ __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) 
 // sub-call are over (previous kernel), and no other item looks for the same key, so the only
 // thing a concurrent claim can be mistaken for is code 0 (a claimed slot whose code is not
 // written yet reads as 0): code-0 keys wait for bulk_zero_kernel. Returns 1 for a claim.
-__device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, uint32_t code, int c,
+__device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, uint64_t code, int c,
                                                int32_t lp) {
   const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
   const uint8_t* v = a.values + (p * a.T + a.s0 + c * kChunk + lp) * a.vbytes;
@@ -899,12 +986,13 @@ __device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, ui
   return r > 0 ? 1 : 0;
 }
 
-// A word of the group table: its code's latest key is in the highest chunk of its mask.
-__device__ __forceinline__ int bulk_insert_word(const StoreArgs& a, const BulkWs& w, int64_t p,
-                                                unsigned long long word) {
-  const uint32_t code = gt_code(word);
-  const int c2 = 31 - __clz(static_cast<uint32_t>(word >> 32));
-  const int32_t lp = chunk_find(w, p, c2, code);
+// A code of the group table with its chunk mask: its latest key is in the highest chunk of
+// the mask.
+template <typename CodeT>
+__device__ __forceinline__ int bulk_insert_masked(const StoreArgs& a, const BulkWs& w, int64_t p,
+                                                  CodeT code, uint32_t mask) {
+  const int c2 = 31 - __clz(mask);
+  const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
   if (lp < 0) {  // the summary of a chunk in the mask holds the code; fail loudly
     atomicOr(a.full, 2);
     return 0;
@@ -912,34 +1000,50 @@ __device__ __forceinline__ int bulk_insert_word(const StoreArgs& a, const BulkWs
   return bulk_insert_key(a, p, code, c2, lp);
 }
 
-// One lane per word of the group table; a workgroup's 256 words lie in one quarter (quarters
-// are at least 256 words). A spilled quarter's workgroups instead take the (chunk, summary
-// slot) pairs of the partition whose code falls in the quarter and insert those whose code no
-// later chunk holds. Each workgroup writes its number of claims to `claims`, and
+// One lane per entry of the group table; a workgroup's 256 entries lie in one part (parts are
+// at least 256 entries). With 64-bit codes the first lane of the all-ones code's part also
+// inserts that code (it has no entry). A spilled part's workgroups instead take the (chunk,
+// summary slot) pairs of the partition whose code falls in the part and insert those whose
+// code no later chunk holds. Each workgroup writes its number of claims to `claims`, and
 // bulk_zero_kernel adds a partition's numbers to its count once: a partition's workgroups run
 // close together in time, so atomics on its count would serialise.
+template <typename CodeT>
 __global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w) {
+  constexpr int kParts = GtTraits<CodeT>::kParts;
   __shared__ uint32_t n_claims;
+  const CodeT SENT = sentinel<CodeT>();
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t p = g >> w.cap_log2;
-  const int qt = static_cast<int>((g & (w.cap - 1)) / w.sub);
+  const int64_t in_p = g & (w.cap - 1);
+  const int qt = static_cast<int>(in_p >> (w.cap_log2 - GtTraits<CodeT>::kPartLog2));
+  const int64_t in_q = in_p & (w.sub - 1);
   if (threadIdx.x == 0) n_claims = 0;
   __syncthreads();
   int claimed = 0;
-  if (!w.spilled[p * kQuarters + qt]) {
-    const unsigned long long word = w.gt[g];
-    if (word != 0 && gt_code(word) != 0) claimed = bulk_insert_word(a, w, p, word);
+  if (!w.spilled[p * kParts + qt]) {
+    if constexpr (sizeof(CodeT) == 4) {
+      const unsigned long long word = w.gt[g];
+      if (word != 0 && gt_code(word) != 0)
+        claimed = bulk_insert_masked<CodeT>(a, w, p, gt_code(word), static_cast<uint32_t>(word >> 32));
+    } else {
+      const CodeT code = w.gt[g];
+      if (code != SENT && code != 0) claimed = bulk_insert_masked<CodeT>(a, w, p, code, w.gmask[g]);
+      if (in_q == 0 && gt_part<CodeT>(splitmix_fin(SENT)) == qt) {
+        const uint32_t m = w.smask[p * kParts + qt];
+        if (m) claimed += bulk_insert_masked<CodeT>(a, w, p, SENT, m);
+      }
+    }
   } else {
     const int per_chunk = kSlots + 1;
-    const int64_t lanes = w.sub;  // the quarter's lanes, one per word
-    for (int64_t q = (g & (w.sub - 1)); q < static_cast<int64_t>(w.nch) * per_chunk; q += lanes) {
+    for (int64_t q = in_q; q < static_cast<int64_t>(w.nch) * per_chunk; q += w.sub) {
       const int c = static_cast<int>(q / per_chunk);
       const int x = static_cast<int>(q - static_cast<int64_t>(c) * per_chunk);
-      uint32_t code;
-      if (!summary_slot(w, p, c, x, code) || code == 0 || gt_quarter(splitmix_fin(code)) != qt)
+      CodeT code;
+      if (!summary_slot<CodeT>(w, p, c, x, code) || code == 0 ||
+          gt_part<CodeT>(splitmix_fin(code)) != qt)
         continue;
       bool later = false;
-      for (int c2 = c + 1; c2 < w.nch && !later; ++c2) later = chunk_find(w, p, c2, code) >= 0;
+      for (int c2 = c + 1; c2 < w.nch && !later; ++c2) later = chunk_find<CodeT>(w, p, c2, code) >= 0;
       if (later) continue;
       const int64_t sum = p * w.nch + c;
       claimed += bulk_insert_key(a, p, code, c, w.sum_pos[sum * kSumPos + x]);
@@ -955,7 +1059,9 @@ __global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w)
 
 // One workgroup per partition: the insert of code 0, then the partition's claims of the
 // sub-call (its workgroup numbers, and code 0's) added to its count.
+template <typename CodeT>
 __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, int32_t blocks_per_part) {
+  constexpr int kParts = GtTraits<CodeT>::kParts;
   __shared__ uint32_t total;
   const int64_t p = blockIdx.x;
   const int t = threadIdx.x;
@@ -963,14 +1069,17 @@ __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, i
   __syncthreads();
   if (t == 0) {
     int r = 0;
-    if (!w.spilled[p * kQuarters + gt_quarter(splitmix_fin(0))]) {
+    if (!w.spilled[p * kParts + gt_part<CodeT>(splitmix_fin(CodeT(0)))]) {
       const int64_t g = w.zero_slot[p];
-      if (g >= 0) r = bulk_insert_word(a, w, p, w.gt[g]);
-    } else {  // spilled quarter: code 0's latest chunk from the summaries
+      if (g >= 0) {
+        const uint32_t m = sizeof(CodeT) == 4 ? static_cast<uint32_t>(w.gt[g] >> 32) : w.gmask[g];
+        r = bulk_insert_masked<CodeT>(a, w, p, CodeT(0), m);
+      }
+    } else {  // spilled part: code 0's latest chunk from the summaries
       for (int c = w.nch - 1; c >= 0; --c) {
-        const int32_t lp = chunk_find(w, p, c, 0u);
+        const int32_t lp = chunk_find<CodeT>(w, p, c, CodeT(0));
         if (lp >= 0) {
-          r = bulk_insert_key(a, p, 0u, c, lp);
+          r = bulk_insert_key(a, p, 0ull, c, lp);
           break;
         }
       }
@@ -986,45 +1095,52 @@ __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, i
 
 // Workspace layout of a bulk call of P partitions (sub-calls of S positions).
 struct BulkLayout {
-  int64_t cap, cap_log2, nch, off_spill, off_zero, off_scode, off_spos, off_src, off_qlist,
-      off_qcount, off_claims, off_filter, bytes;
+  int64_t cap, cap_log2, nch, off_gmask, off_smask, off_spill, off_zero, off_scode, off_spos,
+      off_src, off_qlist, off_qcount, off_claims, off_filter, bytes;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-BulkLayout bulk_layout(int64_t P, int64_t T) {
+BulkLayout bulk_layout(int64_t P, int64_t T, int32_t code_bytes) {
   BulkLayout L{};
+  const int64_t parts = code_bytes == 4 ? GtTraits<uint32_t>::kParts : GtTraits<uint64_t>::kParts;
   const int64_t S = T < kBulkSpan ? T : kBulkSpan;
-  L.cap = 1024;
-  L.cap_log2 = 10;
+  L.cap = 256 * parts;
+  L.cap_log2 = code_bytes == 4 ? 10 : 11;
   while (L.cap < 2 * S) {
     L.cap <<= 1;
     ++L.cap_log2;
   }
   L.nch = (S + kChunk - 1) / kChunk;
   int64_t o = align256(P * L.cap * 8);
+  L.off_gmask = o;
+  o += code_bytes == 8 ? align256(P * L.cap * 4) : 0;
+  L.off_smask = o;
+  o += align256(P * parts * 4);
   L.off_spill = o;
-  o += align256(P * kQuarters * 4);
+  o += align256(P * parts * 4);
   L.off_zero = o;
   o += align256(P * 8);
   L.off_scode = o;
-  o += align256(P * L.nch * kSlots * 4);
+  o += align256(P * L.nch * kSlots * code_bytes);
   L.off_spos = o;
   o += align256(P * L.nch * kSumPos * 4);
   L.off_src = o;
   o += align256(P * S * 4);
   L.off_qlist = o;
-  o += align256(P * L.nch * kQuarters * kChunk * 4);
+  o += align256(P * L.nch * parts * kChunk * code_bytes);
   L.off_qcount = o;
-  o += align256(P * L.nch * kQuarters * 4);
+  o += align256(P * L.nch * parts * 4);
   L.off_claims = o;
   o += align256(P * L.cap / 256 * 4);
   L.off_filter = o;
-  o += align256(P * kQuarters * kFilterWordsQ * 4);
+  o += align256(P * parts * kFilterWordsQ * 4);
   L.bytes = o;
   return L;
 }
-static_assert(2 * kBulkSpan / kQuarters <= kQuarterMax, "a quarter fits the LDS table");
+static_assert(2 * kBulkSpan / GtTraits<uint32_t>::kParts <= GtTraits<uint32_t>::kPartMax &&
+                  2 * kBulkSpan / GtTraits<uint64_t>::kParts <= GtTraits<uint64_t>::kPartMax,
+              "a part fits the LDS table");
 
 }  // namespace
 }  // namespace lema
@@ -1033,47 +1149,51 @@ using namespace lema;
 
 namespace {
 
-constexpr int64_t kBulkMinT = 2 * kChunk;  // longer calls with 32-bit codes take the bulk path
+constexpr int64_t kBulkMinT = 2 * kChunk;  // longer calls take the bulk path
 
-bool bulk_applies(int64_t T, int32_t code_bytes) { return code_bytes == 4 && T > kBulkMinT; }
+bool bulk_applies(int64_t T) { return T > kBulkMinT; }
 
+template <typename CodeT>
 int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
+  constexpr int kParts = GtTraits<CodeT>::kParts;
   const int64_t P = a.n / a.T;
-  const BulkLayout L = bulk_layout(P, a.T);
+  const BulkLayout L = bulk_layout(P, a.T, sizeof(CodeT));
   LEMA_REQUIRE(workspace != nullptr && ws_bytes >= L.bytes && aligned(workspace, 256),
                "workspace of %lld bytes (256-byte aligned) needed, got %lld", (long long)L.bytes,
                (long long)ws_bytes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   BulkWs w{};
   w.gt = reinterpret_cast<unsigned long long*>(ws);
+  w.gmask = reinterpret_cast<uint32_t*>(ws + L.off_gmask);
+  w.smask = reinterpret_cast<uint32_t*>(ws + L.off_smask);
   w.spilled = reinterpret_cast<int32_t*>(ws + L.off_spill);
   w.zero_slot = reinterpret_cast<int64_t*>(ws + L.off_zero);
-  w.sum_code = reinterpret_cast<uint32_t*>(ws + L.off_scode);
+  w.sum_code = ws + L.off_scode;
   w.sum_pos = reinterpret_cast<int32_t*>(ws + L.off_spos);
   w.src_in = reinterpret_cast<int32_t*>(ws + L.off_src);
-  w.qlist = reinterpret_cast<uint32_t*>(ws + L.off_qlist);
+  w.qlist = ws + L.off_qlist;
   w.qcount = reinterpret_cast<int32_t*>(ws + L.off_qcount);
   w.claims = reinterpret_cast<uint32_t*>(ws + L.off_claims);
   w.filter = reinterpret_cast<uint32_t*>(ws + L.off_filter);
   w.cap = static_cast<int32_t>(L.cap);
   w.cap_log2 = static_cast<int32_t>(L.cap_log2);
-  w.sub = static_cast<int32_t>(L.cap / kQuarters);
-  const int32_t blocks_per_part = static_cast<int32_t>(L.cap / 256);  // whole: cap >= 1024
+  w.sub = static_cast<int32_t>(L.cap / kParts);
+  const int32_t blocks_per_part = static_cast<int32_t>(L.cap / 256);  // whole: cap >= 256 * kParts
   for (int64_t s0 = 0; s0 < a.T; s0 += kBulkSpan) {
     a.s0 = s0;
     a.len = static_cast<int32_t>(a.T - s0 < kBulkSpan ? a.T - s0 : kBulkSpan);
     w.nch = (a.len + kChunk - 1) / kChunk;
-    bulk_chunk_kernel<<<dim3(P * w.nch), dim3(kThreads), 0, st>>>(a, w);
+    bulk_chunk_kernel<CodeT><<<dim3(P * w.nch), dim3(kThreads), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_chunk_kernel")) return rc;
-    bulk_table_kernel<<<dim3(P * kQuarters), dim3(kTableThreads), 0, st>>>(w);
+    bulk_table_kernel<CodeT><<<dim3(P * kParts), dim3(kTableThreads), 0, st>>>(w);
     if (int rc = launch_status("bulk_table_kernel")) return rc;
     if (a.qc != nullptr) {
-      bulk_query_kernel<<<dim3((P * a.len + 255) / 256), dim3(256), 0, st>>>(a, w);
+      bulk_query_kernel<CodeT><<<dim3((P * a.len + 255) / 256), dim3(256), 0, st>>>(a, w);
       if (int rc = launch_status("bulk_query_kernel")) return rc;
     }
-    bulk_insert_kernel<<<dim3(P * blocks_per_part), dim3(256), 0, st>>>(a, w);
+    bulk_insert_kernel<CodeT><<<dim3(P * blocks_per_part), dim3(256), 0, st>>>(a, w);
     if (int rc = launch_status("bulk_insert_kernel")) return rc;
-    bulk_zero_kernel<<<dim3(P), dim3(256), 0, st>>>(a, w, blocks_per_part);
+    bulk_zero_kernel<CodeT><<<dim3(P), dim3(256), 0, st>>>(a, w, blocks_per_part);
     if (int rc = launch_status("bulk_zero_kernel")) return rc;
   }
   return LEMA_OK;
@@ -1131,10 +1251,11 @@ int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, con
     return launch_status("store_step_kernel");
   }
   LEMA_REQUIRE(P < (int64_t(1) << 31), "too many partitions (%lld)", (long long)P);
-  if (workspace != nullptr && bulk_applies(T, code_bytes)) {
+  if (workspace != nullptr && bulk_applies(T)) {
     LEMA_REQUIRE(P < (int64_t(1) << 31) - 1 && P * (T < kBulkSpan ? T : kBulkSpan) < (int64_t(1) << 31),
                  "too many items per sub-call (%lld partitions)", (long long)P);
-    return run_bulk(a, workspace, ws_bytes, st);
+    return code_bytes == 4 ? run_bulk<uint32_t>(a, workspace, ws_bytes, st)
+                           : run_bulk<uint64_t>(a, workspace, ws_bytes, st);
   }
   for (int64_t s0 = 0; s0 < T; s0 += kChunk) {
     a.s0 = s0;
@@ -1159,8 +1280,9 @@ extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, con
 }
 
 extern "C" int64_t lema_store_workspace_bytes(int64_t n, int64_t T, int32_t code_bytes) {
-  if (T <= 0 || n <= 0 || n % T != 0 || !bulk_applies(T, code_bytes)) return 0;
-  return bulk_layout(n / T, T).bytes;
+  if (T <= 0 || n <= 0 || n % T != 0 || (code_bytes != 4 && code_bytes != 8) || !bulk_applies(T))
+    return 0;
+  return bulk_layout(n / T, T, code_bytes).bytes;
 }
 
 extern "C" int lema_store_exchange_ws(void* table, int64_t cap, int64_t vbytes, const void* qc,

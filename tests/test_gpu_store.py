@@ -200,7 +200,7 @@ def test_decode_steps_in_a_graph_equal_eager(dev):
 
 
 # ------------------------------------------------------------------ the bulk path
-# Calls with int32 codes and T > 2048 run as sub-calls of up to 32768 positions with in-chunk
+# Calls with T > 2048 run as sub-calls of up to 32768 positions with in-chunk
 # resolution, per-chunk key summaries and a scratch table of the sub-call's (partition, code)
 # pairs: the results must be the dict's in every case the chunked path covers.
 
@@ -286,9 +286,9 @@ def _splitmix_fin(x):
     return x ^ (x >> np.uint64(31))
 
 
-def _bulk_group_cap(T):
+def _bulk_group_cap(T, parts=4):
     s = min(T, 32 * 1024)
-    cap = 1024
+    cap = 256 * parts
     while cap < 2 * s:
         cap *= 2
     return cap
@@ -349,63 +349,151 @@ def run_store_rows_case(dev, seed, d_v, P, Ts):
     assert np.array_equal(store.counts.numpy(), ref.counts())
 
 
+def exchange_chunked(st, qc, kc, values, out, T, g0):
+    """The same exchange through lema_store_exchange, which takes no workspace and so runs
+    every call in 1024-position sub-chunks (the bulk path is off)."""
+    from latest_exact_match_attention_amd import _lib
+    L = _lib.lib()
+    cb = kc.element_size()
+    _lib.check(L.lema_store_exchange(
+        st.table.data_ptr(), st.cap, st.vbytes, qc.data_ptr() if qc is not None else None,
+        kc.data_ptr(), cb, values.data_ptr(), out.data_ptr() if out is not None else None,
+        kc.numel(), T, g0, st.counts_device.data_ptr(), st.full_flag.data_ptr(),
+        _lib.stream_of(kc)))
+    st.check_full()
+
+
+def _three_paths(dev, qc, kc, v, P, T, cap):
+    """Outputs, stores and counts of one exchange through the bulk path with int32 and int64
+    codes and through the chunked path."""
+    res = []
+    for dt, bulk in ((torch.int32, True), (torch.int64, True), (torch.int64, False)):
+        st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+        out = torch.empty_like(v)
+        q, k = torch.from_numpy(qc).to(dev).to(dt), torch.from_numpy(kc).to(dev).to(dt)
+        if bulk:
+            st.exchange(q, k, v, out, T, 0)
+        else:
+            exchange_chunked(st, q, k, v, out, T, 0)
+        res.append((out, st))
+    return res
+
+
 def test_bulk_equals_chunked_path_and_insert_only(dev):
-    """The same long exchange through the bulk path (int32 codes) and the chunked path (int64
-    codes of the same values) leaves the same entries and returns the same values; an
-    insert-only long call then serves later queries."""
+    """The same long exchange through the bulk path (int32 and int64 codes of the same values)
+    and the chunked path leaves the same entries and returns the same values; an insert-only
+    long call then serves later queries."""
     rng = np.random.default_rng(15)
     P, T, cap = 6, 8192, 60_000
     qc = rng.integers(0, 3000, size=P * T)
     kc = rng.integers(0, 3000, size=P * T)
     v = torch.from_numpy(rng.integers(-30000, 30000, size=(P * T, D_V), dtype=np.int16)).to(dev)
     dumps, outs = [], []
-    for dt in (torch.int32, torch.int64):
-        st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
-        out = torch.empty_like(v)
-        st.exchange(torch.from_numpy(qc).to(dev).to(dt), torch.from_numpy(kc).to(dev).to(dt),
-                    v, out, T, 0)
+    for out, st in _three_paths(dev, qc, kc, v, P, T, cap):
         g, c, val = st.dump()
         dumps.append({(int(a), int(b)): bytes(x) for a, b, x in
                       zip(g.cpu().numpy(), c.cpu().numpy(), val.cpu().numpy())})
         outs.append(out)
-    assert torch.equal(outs[0], outs[1]) and dumps[0] == dumps[1]
-    st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
-    st.exchange(None, torch.from_numpy(kc).to(dev).to(torch.int32), v, None, T, 0)
-    q = torch.from_numpy(kc.reshape(P, T)[:, ::2].copy()).to(dev).to(torch.int32).reshape(-1)
-    got = torch.empty((q.numel(), D_V), dtype=torch.int16, device=dev)
-    st.exchange(q, torch.full_like(q, -7), torch.zeros_like(got), got, T // 2, 0)
-    ref = oracle.DictStore(P, 2 * D_V)
-    vv = v.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V)
-    ref.exchange(np.full(P * T, -123), kc, vv, T, 0)
-    want = ref.exchange(q.cpu().numpy().astype(np.int64), np.full(q.numel(), (1 << 32) - 7),
-                        np.zeros((q.numel(), 2 * D_V), np.uint8), T // 2, 0)
-    assert np.array_equal(got.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want)
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    assert all(dumps[0] == d for d in dumps[1:])
+    for dt in (torch.int32, torch.int64):
+        st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+        st.exchange(None, torch.from_numpy(kc).to(dev).to(dt), v, None, T, 0)
+        q = torch.from_numpy(kc.reshape(P, T)[:, ::2].copy()).to(dev).to(dt).reshape(-1)
+        got = torch.empty((q.numel(), D_V), dtype=torch.int16, device=dev)
+        st.exchange(q, torch.full_like(q, -7), torch.zeros_like(got), got, T // 2, 0)
+        ref = oracle.DictStore(P, 2 * D_V)
+        vv = v.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V)
+        ref.exchange(np.full(P * T, -123), kc, vv, T, 0)
+        k7 = (1 << 32) - 7 if dt == torch.int32 else -7
+        want = ref.exchange(q.cpu().numpy().astype(np.int64), np.full(q.numel(), k7),
+                            np.zeros((q.numel(), 2 * D_V), np.uint8), T // 2, 0)
+        assert np.array_equal(got.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want), dt
 
 
 def test_bulk_many_partitions_equals_chunked_path(dev):
-    """4,200 partitions x T = 2,100 (4,200 regions of the scratch table, each partition's
-    claims tallied from its region's workgroups): the bulk path (int32 codes) and the chunked
-    path (int64 codes) agree on outputs, entries and per-partition counts."""
+    """4,200 partitions x T = 2,100 (4,200 group tables, each partition's claims tallied from
+    its workgroups): the bulk path (int32 and int64 codes) and the chunked path agree on
+    outputs, entries and per-partition counts."""
     rng = np.random.default_rng(16)
     P, T, cap = 4200, 2100, 9_000_000
     qc = rng.integers(0, 700, size=P * T)
     kc = rng.integers(0, 700, size=P * T)
     v = torch.from_numpy(rng.integers(-30000, 30000, size=(P * T, D_V), dtype=np.int16)).to(dev)
     outs, dumps, counts = [], [], []
-    for dt in (torch.int32, torch.int64):
-        st = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
-        out = torch.empty_like(v)
-        st.exchange(torch.from_numpy(qc).to(dev).to(dt), torch.from_numpy(kc).to(dev).to(dt),
-                    v, out, T, 0)
+    for out, st in _three_paths(dev, qc, kc, v, P, T, cap):
         g, c, val = st.dump()
         key = g * 1024 + c                                   # codes < 700, groups < 4200
         order = torch.argsort(key)
         dumps.append((key[order], val[order]))
         outs.append(out)
         counts.append(st.counts)
-    assert torch.equal(outs[0], outs[1])
-    assert torch.equal(dumps[0][0], dumps[1][0]) and torch.equal(dumps[0][1], dumps[1][1])
-    assert torch.equal(counts[0], counts[1]) and int(counts[0].sum()) == dumps[0][0].numel()
+    for i in (1, 2):
+        assert torch.equal(outs[0], outs[i])
+        assert torch.equal(dumps[0][0], dumps[i][0]) and torch.equal(dumps[0][1], dumps[i][1])
+        assert torch.equal(counts[0], counts[i])
+    assert int(counts[0].sum()) == dumps[0][0].numel()
+
+
+def test_bulk_64bit_codes_all_ones_and_zero(dev):
+    """64-bit codes through the bulk path: the all-ones code (int64 -1, the group table's
+    free marker, kept apart there) and 0 are codes like any other, beside codes with high
+    bits set, against the dict over two long calls."""
+    rng = np.random.default_rng(19)
+    P, T = 4, 6000
+    pool = np.array([-1, 0, 1, -2, (1 << 62) + 5, -(1 << 40), 123456789012345], dtype=np.int64)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=20_000, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    for call in range(2):
+        qc = rng.choice(pool, size=P * T)
+        kc = rng.choice(pool, size=P * T)
+        far = rng.random(P * T) < 0.3
+        qc[far] = rng.integers(1 << 40, 1 << 62, size=int(far.sum()))
+        vals = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+        out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev),
+                       torch.from_numpy(vals.view(np.int16)).to(dev), out, T, 0)
+        want = ref.exchange(qc, kc, vals.view(np.uint8).reshape(-1, 2 * D_V), T, 0)
+        assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want), call
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    assert set(store.dump()[1].cpu().numpy().astype(np.int64).tolist()) == set(pool.tolist())
+
+
+def test_bulk_64bit_spilled_part(dev):
+    """64-bit key codes chosen so that one of a partition's eight group-table parts gets more
+    codes than its LDS table takes: that part's queries and inserts search the chunk
+    summaries. One spilled partition holds code 0 in that part, another the all-ones code;
+    beside them an unspilled part and ordinary codes, two calls against the dict."""
+    rng = np.random.default_rng(20)
+    P, T = 4, 6000
+    cand = rng.integers(-(1 << 62), 1 << 62, size=400_000, dtype=np.int64) * 2 + 1
+    part_of = lambda c: _splitmix_fin(np.asarray(c, dtype=np.int64).view(np.uint64)) >> np.uint64(61)
+    part = part_of(cand)
+    z, s = int(part_of(0)), int(part_of(-1))        # the parts of code 0 and the all-ones code
+    pz, ps = cand[part == z], cand[part == s]
+    pools = [np.concatenate([[0], pz[:5000]]),     # fills code 0's part
+             np.concatenate([[-1], ps[:5000]]),    # fills the all-ones code's part
+             pz[5000:5300],                        # the same part as the first, few codes
+             cand[:3000]]                          # ordinary codes
+    limit = _bulk_group_cap(T, parts=8) // 8 // 4 * 3
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=300_000, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    for call in range(2):
+        kc = np.concatenate([rng.choice(pool, size=T) for pool in pools])
+        assert len(set(kc[:T].tolist())) > limit and len(set(kc[T:2 * T].tolist())) > limit
+        assert len(set(kc[2 * T:3 * T].tolist())) < limit
+        kc[[0, T + 1]] = [0, -1]                   # both special codes are keys
+        qc = np.concatenate([rng.choice(pool, size=T) for pool in pools])
+        miss = rng.random(P * T) < 0.2
+        qc[miss] = rng.integers(1 << 40, 1 << 62, size=int(miss.sum())) * 2
+        vals = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+        out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev),
+                       torch.from_numpy(vals.view(np.int16)).to(dev), out, T, 0)
+        want = ref.exchange(qc, kc, vals.view(np.uint8).reshape(-1, 2 * D_V), T, 0)
+        assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want), call
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    store.check_full()
 
 
 @pytest.mark.parametrize("d_v,dtype", [(4, np.float16), (12, np.float16), (2, np.float32)])
