@@ -435,6 +435,28 @@ def test_bulk_many_partitions_equals_chunked_path(dev):
     assert int(counts[0].sum()) == dumps[0][0].numel()
 
 
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_bulk_group_offsets(dev, code_dtype):
+    """Long calls at non-zero group offsets (a layer's partitions start at layer x B x H):
+    groups [5, 8) then [0, 5) then [2, 10) of one 10-group store, overlapping, against the dict;
+    entries of different groups with equal codes stay apart, and counts land on the right
+    groups."""
+    rng = np.random.default_rng(21)
+    store = HashStore(D_V, groups=10, dtype=np.uint16, capacity=200_000, device=dev)
+    ref = oracle.DictStore(10, 2 * D_V)
+    for g0, P, T in ((5, 3, 5000), (0, 5, 3000), (2, 8, 2600)):
+        qc = rng.integers(0, 4000, size=P * T)
+        kc = rng.integers(0, 4000, size=P * T)
+        vals = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+        out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev).to(code_dtype),
+                       torch.from_numpy(kc).to(dev).to(code_dtype),
+                       torch.from_numpy(vals.view(np.int16)).to(dev), out, T, g0)
+        want = ref.exchange(qc, kc, vals.view(np.uint8).reshape(-1, 2 * D_V), T, g0)
+        assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want), g0
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+
+
 def test_bulk_64bit_codes_all_ones_and_zero(dev):
     """64-bit codes through the bulk path: the all-ones code (int64 -1, the group table's
     free marker, kept apart there) and 0 are codes like any other, beside codes with high
