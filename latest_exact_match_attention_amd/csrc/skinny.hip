@@ -44,7 +44,16 @@ struct SkSegment {
   const uint16_t* res; // plain: optional bf16 [M, ldy] residual, out = bf16(res + bf16(sum))
   int64_t ldy;
   int32_t N, mode, blocks, code_bytes;
+  int32_t cols;        // output columns per block (set at launch; swiglu: of the gate and of up)
 };
+
+// A product on few blocks leaves CUs idle, and each block's weight read is bound by what its
+// CU keeps in flight (measured at M = 1, K = 1536: 96 and 192 blocks of 16 columns both take
+// 3.9 us). A launch of plain segments only (16-column tiles) with at most kNarrowMaxN columns
+// therefore takes blocks of 8 columns, the other half of each matrix-core tile idle. In the
+// q/k/v launch the packed q and k blocks (whole heads) are the longest, so v keeps its width.
+constexpr int kNarrowCols = 8;
+constexpr int kNarrowMaxN = 256 * kNarrowCols;
 
 struct SkinnyArgs {
   const uint16_t* x;
@@ -67,7 +76,8 @@ __device__ __forceinline__ bool bf16_nonneg(float z) {
   return bf16_bits_to_f32(f32_to_bf16_bits(z)) >= 0.0f;
 }
 
-// A block owns 16 * CT columns (swiglu: 16 columns of the gate and the same 16 of up).
+// A block owns `cols` columns: 16 * CT, or 8 for a narrow plain segment (swiglu: 16 columns
+// of the gate and the same 16 of up).
 template <int MT, int CT>
 __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   __shared__ float part[kSkWaves][MT * 16][CT * 16 + 1];
@@ -79,7 +89,8 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   const SkSegment& sg = a.seg[si];
   const bool glu = sg.mode == kSkSwiglu;
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int n0 = bid * (glu ? 16 : CT * 16);
+  const int cols = sg.cols;
+  const int n0 = bid * cols;
   const int ksteps = a.K / 32;
   const int per = (ksteps + kSkWaves - 1) / kSkWaves;
   const int s0 = wave * per;
@@ -90,8 +101,9 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   bool wok[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const int n = glu ? n0 + r16 : n0 + 16 * ct + r16;
-    wok[ct] = n < sg.N && (!glu || ct < 2);
+    const int c = glu ? r16 : 16 * ct + r16;  // column of the block
+    const int n = n0 + c;
+    wok[ct] = c < cols && n < sg.N && (!glu || ct < 2);
     const uint16_t* base = (glu && ct == 1) ? sg.w2 : sg.w;
     wp[ct] = base + static_cast<int64_t>(wok[ct] ? n : 0) * a.ldw + kg;
   }
@@ -157,7 +169,7 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
     for (int i = 0; i < kPer; ++i) {
       const int e = threadIdx.x + i * kSkThreads;
       const int row = e / kCols, col = e - (e / kCols) * kCols;
-      if (e < kRows * kCols && row < a.M && n0 + col < sg.N) {
+      if (e < kRows * kCols && row < a.M && col < cols && n0 + col < sg.N) {
         const int64_t at = static_cast<int64_t>(row) * sg.ldy + n0 + col;
         uint32_t out = f32_to_bf16_bits(sums[i]);
         if (sg.res != nullptr) out = f32_to_bf16_bits(bf16_bits_to_f32(sg.res[at]) + bf16_bits_to_f32(out));
@@ -177,7 +189,7 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
     uint16_t* y = static_cast<uint16_t*>(sg.out);
     for (int e = threadIdx.x; e < kRows * 16; e += kSkThreads) {
       const int row = e >> 4, c = e & 15;
-      if (row >= a.M || n0 + c >= sg.N) continue;
+      if (row >= a.M || c >= cols || n0 + c >= sg.N) continue;
       const float g = bf16_bits_to_f32(f32_to_bf16_bits(part[0][row][c]));
       const float u = bf16_bits_to_f32(f32_to_bf16_bits(part[0][row][16 + c]));
       const float sl = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.0f + expf(-g))));
@@ -207,9 +219,12 @@ template <int CT>
 int launch_skinny(SkinnyArgs& a, hipStream_t st) {
   int blocks = 0;
   for (int i = 0; i < a.nseg; ++i) {
-    const int cols = a.seg[i].mode == kSkSwiglu ? 16 : 16 * CT;
-    a.seg[i].blocks = (a.seg[i].N + cols - 1) / cols;
-    blocks += a.seg[i].blocks;
+    SkSegment& sg = a.seg[i];
+    sg.cols = sg.mode == kSkSwiglu ? 16
+              : CT == 1 && sg.mode == kSkPlain && sg.N <= kNarrowMaxN ? kNarrowCols
+                                                                     : 16 * CT;
+    sg.blocks = (sg.N + sg.cols - 1) / sg.cols;
+    blocks += sg.blocks;
   }
   const dim3 grid(blocks), block(kSkThreads);
   if (a.M <= 16)
