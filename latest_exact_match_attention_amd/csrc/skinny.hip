@@ -10,10 +10,10 @@
 // k and v projections):
 //   plain   Y rounded to bf16, optionally added to a bf16 residual (the MLP's down projection
 //           and the residual add of Block.forward, code/lema/model.py:229-232);
-//   pack    the q or k projection straight to codes (code/lema/attention.py:82-97): the block
-//           covers whole heads of d columns, and bit j of a head's code is (bf16(z_j) >= 0),
-//           the sign of the value the unfused path would have stored -- the projection's
-//           output never goes to HBM;
+//   pack    the q or k projection straight to codes (code/lema/attention.py:82-97): bit j of a
+//           head's code is (bf16(z_j) >= 0), the sign of the value the unfused path would have
+//           stored -- the projection's output never goes to HBM. A block covers 16 columns and
+//           writes the bytes of each code its columns hold (d a multiple of 8), or whole heads;
 //   swiglu  silu(x . gate^T) * (x . up^T) with the same bf16 roundings as SwiGLU.forward's
 //           ops (code/lema/model.py:85-94): the block computes 16 columns of both.
 //
@@ -50,8 +50,8 @@ struct SkSegment {
 // A product on few blocks leaves CUs idle, and each block's weight read is bound by what its
 // CU keeps in flight (measured at M = 1, K = 1536: 96 and 192 blocks of 16 columns both take
 // 3.9 us). A launch of plain segments only (16-column tiles) with at most kNarrowMaxN columns
-// therefore takes blocks of 8 columns, the other half of each matrix-core tile idle. In the
-// q/k/v launch the packed q and k blocks (whole heads) are the longest, so v keeps its width.
+// therefore takes blocks of 8 columns, the other half of each matrix-core tile idle. A launch
+// with packed segments (q/k/v) already has three segments' blocks and keeps 16 columns.
 constexpr int kNarrowCols = 8;
 constexpr int kNarrowMaxN = 256 * kNarrowCols;
 
@@ -197,21 +197,34 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
     }
     return;
   }
-  const int heads = kCols / a.d;  // whole heads per block (checked on the host)
+  // the heads this block's columns [n0, n0 + cols) touch; a head split over blocks gets its
+  // byte-aligned bit range written by each (d is a multiple of 8 then, checked on the host),
+  // the block with its last bit also clearing the code's bytes above d
   const int H = sg.N / a.d;
-  for (int e = threadIdx.x; e < kRows * heads; e += kSkThreads) {
-    const int row = e / heads, hh = e - (e / heads) * heads;
-    const int h = n0 / a.d + hh;
-    if (row >= a.M || h >= H) continue;
+  const int h0 = n0 / a.d;
+  const int h1 = min((n0 + cols - 1) / a.d, H - 1);
+  const int nh = h1 - h0 + 1;
+  for (int e = threadIdx.x; e < kRows * nh; e += kSkThreads) {
+    const int row = e / nh, h = h0 + (e - (e / nh) * nh);
+    if (row >= a.M) continue;
+    const int c_lo = max(n0, h * a.d), c_hi = min(n0 + cols, (h + 1) * a.d);
     uint64_t code = 0;
-    for (int j = 0; j < a.d; ++j)
-      if (bf16_nonneg(part[0][row][hh * a.d + j])) code |= uint64_t(1) << j;
+    for (int n = c_lo; n < c_hi; ++n)
+      if (bf16_nonneg(part[0][row][n - n0])) code |= uint64_t(1) << (n - h * a.d);
     const int64_t b = row / a.T, t = row - (row / a.T) * a.T;
     const int64_t at = (b * H + h) * a.T + t;
-    if (sg.code_bytes == 4)
-      static_cast<uint32_t*>(sg.out)[at] = static_cast<uint32_t>(code);
-    else
-      static_cast<uint64_t*>(sg.out)[at] = code;
+    const int j_lo = c_lo - h * a.d, j_hi = c_hi - h * a.d;  // bits [j_lo, j_hi) of the code
+    if (j_lo == 0 && j_hi == a.d) {
+      if (sg.code_bytes == 4)
+        static_cast<uint32_t*>(sg.out)[at] = static_cast<uint32_t>(code);
+      else
+        static_cast<uint64_t*>(sg.out)[at] = code;
+    } else {
+      uint8_t* w8 = static_cast<uint8_t*>(sg.out) + at * sg.code_bytes;
+      for (int k = j_lo / 8; k < j_hi / 8; ++k) w8[k] = static_cast<uint8_t>(code >> (8 * k));
+      if (j_hi == a.d)
+        for (int k = a.d / 8; k < sg.code_bytes; ++k) w8[k] = 0;
+    }
   }
 }
 
@@ -220,9 +233,11 @@ int launch_skinny(SkinnyArgs& a, hipStream_t st) {
   int blocks = 0;
   for (int i = 0; i < a.nseg; ++i) {
     SkSegment& sg = a.seg[i];
+    bool all_plain = true;
+    for (int j = 0; j < a.nseg; ++j) all_plain = all_plain && a.seg[j].mode == kSkPlain;
     sg.cols = sg.mode == kSkSwiglu ? 16
-              : CT == 1 && sg.mode == kSkPlain && sg.N <= kNarrowMaxN ? kNarrowCols
-                                                                     : 16 * CT;
+              : CT == 1 && all_plain && sg.N <= kNarrowMaxN ? kNarrowCols
+                                                           : 16 * CT;
     sg.blocks = (sg.N + sg.cols - 1) / sg.cols;
     blocks += sg.blocks;
   }
@@ -259,9 +274,12 @@ int check_weight(const void* w, int64_t N) {
   return LEMA_OK;
 }
 
-// Columns per block for codes of d bits: the least multiple of 16 (up to 64) holding whole
-// heads, or 0.
+// Column tiles per block for codes of d bits: one (16 columns, a head split over blocks
+// writes its bytes from each) when d is a multiple of 8, else the least multiple of 16 (up to
+// 64) holding whole heads, or 0. More blocks of fewer weight rows: the q and k projections of
+// 64-bit heads ran on 24 blocks of 64 rows each.
 int pack_ct(int32_t d) {
+  if (d % 8 == 0) return 1;
   for (int c = 1; c <= 4; ++c)
     if ((16 * c) % d == 0) return c;
   return 0;

@@ -122,7 +122,9 @@ def project_codes(x: torch.Tensor, lin: nn.Linear, d: int, code_dtype: torch.dty
 
 
 def _pack_tiles(d: int) -> bool:
-    return any((16 * c) % d == 0 for c in (1, 2, 3, 4))
+    """Whether the skinny kernel packs d-bit codes: heads split over 16-column blocks when d
+    is a multiple of 8, else whole heads in blocks of up to 64 columns."""
+    return d % 8 == 0 or any((16 * c) % d == 0 for c in (1, 2, 3, 4))
 
 
 def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype):

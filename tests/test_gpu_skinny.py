@@ -31,21 +31,27 @@ def test_skinny_gemm_matches_fp32(dev, M, N, K):
     assert (err <= 2 ** -8 * ref.abs() + 1e-5).all(), (err / ref.abs().clamp_min(1e-6)).max()
 
 
-@pytest.mark.parametrize("d", [24, 16, 32, 8, 64])
+@pytest.mark.parametrize("d", [24, 16, 32, 8, 64, 40, 48])
 @pytest.mark.parametrize("B,T", [(16, 1), (4, 3), (1, 32)])
 def test_skinny_pack_codes(dev, d, B, T):
+    """Codes of d-bit heads, heads split over 16-column blocks when d is a multiple of 8 (each
+    block writes its bytes of the code): the bits match the packed bf16 projection, and the
+    bits above d are zero although the buffer starts as all ones."""
     H, K = 64, 1536
     g = torch.Generator(device=dev).manual_seed(d + B)
     x = torch.randn(B, T, K, device=dev, generator=g).to(torch.bfloat16)
     w = (torch.randn(H * d, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
     ct = torch.int32 if d <= 32 else torch.int64
-    codes = torch.empty((B, H, T), dtype=ct, device=dev)
+    codes = torch.full((B, H, T), -1, dtype=ct, device=dev)
     _lib.check(_lib.lib().lema_skinny_pack_bf16(x.data_ptr(), K, w.data_ptr(), K, B * T, H * d, K,
                                                 d, T, codes.data_ptr(), codes.element_size(),
                                                 _lib.stream_of(x)))
     z = (x.float().reshape(B * T, K) @ w.float().T).view(B, T, H, d).transpose(1, 2)
     want = torch_model.pack(z.to(torch.bfloat16))
-    got = codes.long() if d == 64 else codes.long() & ((1 << d) - 1)
+    raw = codes.long() & 0xFFFFFFFF if ct == torch.int32 else codes.long()
+    if d < codes.element_size() * 8:
+        assert (raw >> d == 0).all(), "bits above d are set"
+    got = raw
     diff = got ^ want
     if diff.any():                                   # only near-zero pre-activations may flip
         bits = ((diff.unsqueeze(-1) >> torch.arange(d, device=dev)) & 1).bool()
@@ -63,7 +69,8 @@ def pack(x, w, d, T, ct):
     return codes
 
 
-@pytest.mark.parametrize("d,Nv", [(24, 1536), (16, 1024), (32, 2048), (8, 40), (64, 1536)])
+@pytest.mark.parametrize("d,Nv", [(24, 1536), (16, 1024), (32, 2048), (8, 40), (64, 1536),
+                                  (40, 1536), (56, 1536)])
 @pytest.mark.parametrize("B,T", [(16, 1), (4, 3), (1, 1)])
 def test_skinny_qkv_equals_separate_launches(dev, d, Nv, B, T):
     """The one-launch q/k/v projection gives bit for bit what three launches give (each column
