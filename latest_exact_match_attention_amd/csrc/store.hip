@@ -750,22 +750,38 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
   int32_t* spos = w.sum_pos + sum * kSumPos;
   for (int x = t; x < kSlots; x += kThreads) scode[x] = s.code[x];
   for (int x = t; x <= kSlots; x += kThreads) spos[x] = s.pos[x];
+  // each thread's slots first, then per part one LDS atomic per wave reserves the places of
+  // all its codes of that part
   const int lane = t & 63;
+  const unsigned long long below = (1ull << lane) - 1;
   CodeT* lists = static_cast<CodeT*>(w.qlist) + sum * kParts * kChunk;
-  for (int x0 = 0; x0 <= kSlots; x0 += kThreads) {  // the same trip count in every thread
-    const int x = x0 + t;
-    const CodeT code = x < kSlots ? s.code[x] : SENT;
-    const bool held = x < kSlots ? code != SENT : x == kSlots && s.pos[kSlots] >= 0;
-    const int q = held ? gt_part<CodeT>(splitmix_fin(code)) : 0;
+  constexpr int kRounds = (kSlots + 1 + kThreads - 1) / kThreads;
+  CodeT rc[kRounds];
+  int rq[kRounds];  // the slot's part, or -1 when the chunk holds no key with its code
 #pragma unroll
-    for (int qq = 0; qq < kParts; ++qq) {
-      const unsigned long long b = __ballot(held && q == qq);
-      if (b == 0) continue;
-      const int leader = __ffsll(b) - 1;
-      int at = 0;
-      if (lane == leader) at = atomicAdd(&n_in[qq], static_cast<int32_t>(__popcll(b)));
-      at = __shfl(at, leader);
-      if (held && q == qq) lists[qq * kChunk + at + __popcll(b & ((1ull << lane) - 1))] = code;
+  for (int r = 0; r < kRounds; ++r) {
+    const int x = r * kThreads + t;
+    rc[r] = x < kSlots ? s.code[x] : SENT;
+    const bool held = x < kSlots ? rc[r] != SENT : x == kSlots && s.pos[kSlots] >= 0;
+    rq[r] = held ? gt_part<CodeT>(splitmix_fin(rc[r])) : -1;
+  }
+#pragma unroll
+  for (int qq = 0; qq < kParts; ++qq) {
+    unsigned long long bal[kRounds];
+    int total = 0;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      bal[r] = __ballot(rq[r] == qq);
+      total += __popcll(bal[r]);
+    }
+    if (total == 0) continue;  // wave-uniform
+    int at = 0;
+    if (lane == 0) at = atomicAdd(&n_in[qq], total);
+    at = __shfl(at, 0);
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      if (rq[r] == qq) lists[qq * kChunk + at + __popcll(bal[r] & below)] = rc[r];
+      at += __popcll(bal[r]);
     }
   }
   __syncthreads();
