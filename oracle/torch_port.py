@@ -1,4 +1,4 @@
-"""The reference's CPU "library attention" restated with torch ops, for the CPU BASELINE only
+"""The reference's CPU "library attention" restated with torch ops, for the CPU baseline only
 (test infrastructure: the product never imports this).
 
 `latest_prev_match_sorted` follows code/lema/attention.py:100-132 step for step -- two

@@ -1,6 +1,7 @@
 """The LEMA model on the GPU: the exact op inside the model, the HBM cache in any chunking,
 the single-graph decoder, and the forward loss against the functional oracle model
-(code/tests/test_gpu.py:68-90 and 117-141; SURVEY C5 tolerance: loss within 1e-2 relative)."""
+(code/tests/test_gpu.py:68-90 and 117-141; the full-model tolerance: loss within 1e-2
+relative)."""
 import pytest
 import torch
 
