@@ -114,12 +114,14 @@ int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc
                         int64_t g0, int64_t* counts, int32_t* full, void* stream);
 
 /* Workspace bytes lema_store_exchange_ws needs for a call of n items, T positions per
- * partition and code_bytes codes; 0 when such a call does not use one (T <= 2048). No
- * reference counterpart: lema_store_exchange's long calls made parallel. */
+ * partition and code_bytes codes; 0 when such a call does not use one: T <= 1024, or
+ * T <= 2048 with more than 128 partitions, or T <= 4096 with 512 or more (the chunked path is
+ * the faster one there). No reference counterpart: lema_store_exchange's long calls made
+ * parallel. */
 int64_t lema_store_workspace_bytes(int64_t n, int64_t T, int32_t code_bytes);
 
 /* lema_store_exchange with a device workspace (256-byte aligned, at least
- * lema_store_workspace_bytes): a call with T > 2048 then runs in sub-calls of
+ * lema_store_workspace_bytes): a call for which that is non-zero then runs in sub-calls of
  * up to 32768 positions, each as a few kernels over all of its items (in-chunk resolution,
  * per-chunk key summaries and a scratch table of every (partition, code) of the sub-call),
  * instead of one launch per 1024 positions. Same results as lema_store_exchange

@@ -87,6 +87,7 @@ struct StoreArgs {
   int32_t pieces;  // vbytes / piece
   bool pre;        // piece 16 and pieces <= kStepGroup: a decode step preloads the value row
   bool spec;       // piece 16 and pieces <= kSpecPieces: its query window reads whole slots
+  int32_t cg_log2; // log2 of the lanes that copy one row in wave_copy_rows (pieces, up to 16)
   unsigned long long* counts;
   int32_t* full;
 };
@@ -112,6 +113,43 @@ __device__ __forceinline__ void group_copy(const StoreArgs& a, uint8_t* dst, con
     } else {
       const u32x2 v = src ? *reinterpret_cast<const u32x2*>(src + 8 * k) : u32x2{0u, 0u};
       *reinterpret_cast<u32x2*>(dst + 8 * k) = v;
+    }
+  }
+}
+
+// Copy the value rows the lanes of a wave name (lane L: dst_L non-null; src_L null writes
+// zeros), 2^cg_log2 lanes per row, each lane one piece of a row per instruction: an
+// instruction moves whole rows of 64 >> cg_log2 named rows instead of one piece of each of
+// 64 scattered rows, so a row costs one or two line requests rather than one per piece.
+// Named rows are compacted first (lane r of `order` holds the lane naming the r-th row).
+// Every lane of the wave must call it.
+__device__ __forceinline__ void wave_copy_rows(const StoreArgs& a, uint8_t* dst, const uint8_t* src) {
+  const unsigned long long act = __ballot(dst != nullptr);
+  if (act == 0) return;
+  const int lane = static_cast<int>(__lane_id());
+  const int m = __popcll(act);
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const int rank = dst != nullptr ? __popcll(act & below) : m + __popcll(~act & below);
+  const int order = __builtin_amdgcn_ds_permute(rank << 2, lane);  // a permutation of the lanes
+  const int g = 1 << a.cg_log2;
+  const int gl = lane & (g - 1);
+  const int rows = 64 >> a.cg_log2;  // rows per pass; r0 + lane / g stays below 64
+  for (int r0 = 0; r0 < m; r0 += rows) {
+    const int r = r0 + (lane >> a.cg_log2);
+    const int owner = __shfl(order, r);
+    uint8_t* d = reinterpret_cast<uint8_t*>(__shfl(reinterpret_cast<unsigned long long>(dst), owner));
+    const uint8_t* sp =
+        reinterpret_cast<const uint8_t*>(__shfl(reinterpret_cast<unsigned long long>(src), owner));
+    if (r < m) {
+      for (int k = gl; k < a.pieces; k += g) {
+        if (a.piece == 16) {
+          const u32x4 v = sp ? *reinterpret_cast<const u32x4*>(sp + 16 * k) : u32x4{0u, 0u, 0u, 0u};
+          *reinterpret_cast<u32x4*>(d + 16 * k) = v;
+        } else {
+          const u32x2 v = sp ? *reinterpret_cast<const u32x2*>(sp + 8 * k) : u32x2{0u, 0u};
+          *reinterpret_cast<u32x2*>(d + 8 * k) = v;
+        }
+      }
     }
   }
 }
@@ -493,27 +531,13 @@ __device__ int64_t lane_lookup(const StoreArgs& a, uint64_t code, uint64_t tag, 
   return -1;
 }
 
-// The value of a slot: from registers (`vals`, when the row is at most kSpecPieces 16-byte
-// pieces: a.spec) or copied from `value`.
-__device__ __forceinline__ void lane_put_value(const StoreArgs& a, int64_t s, const uint8_t* value,
-                                               const u32x4 (&vals)[kSpecPieces]) {
-  uint8_t* dst = a.table + s * a.stride + 16;
-  if (a.spec) {
-#pragma unroll
-    for (int k = 0; k < kSpecPieces; ++k)
-      if (k < a.pieces) *reinterpret_cast<u32x4*>(dst + 16 * k) = vals[k];
-  } else {
-    group_copy<1>(a, dst, value, 0);
-  }
-}
-
-// Insert (tag, code) -> value (code/lema/csrc/store.cpp:97-117) from home slot `base`: 1 =
-// claimed a new slot, 0 = overwrote the partition's entry, -1 = probed every slot without room.
-// No other lane inserts the same key at the same time, so a claim lost to a race is another
-// key's slot, and every slot that read free was free before the kernel, so the key cannot lie
-// beyond it: the probe goes on to claim.
-__device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, const uint8_t* value,
-                           const u32x4 (&vals)[kSpecPieces], int64_t base) {
+// Insert (tag, code) (code/lema/csrc/store.cpp:97-117) from home slot `base`: 1 = claimed a
+// new slot, 0 = found the partition's entry, -1 = probed every slot without room. `slot` is
+// the slot whose value the caller writes. No other lane inserts the same key at the same time,
+// so a claim lost to a race is another key's slot, and every slot that read free was free
+// before the kernel, so the key cannot lie beyond it: the probe goes on to claim.
+__device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, int64_t base,
+                           int64_t& slot) {
   PairHead p = load_pair(a, base, a.cap);
   for (int64_t left = a.cap; left > 0;) {
 #pragma unroll
@@ -521,14 +545,14 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, cons
       if (k >= p.width) break;
       const int64_t s = base + k >= a.cap ? base + k - a.cap : base + k;
       if (p.s[k] == tag && p.c[k] == code) {
-        lane_put_value(a, s, value, vals);
+        slot = s;
         return 0;
       }
       if (p.s[k] == kStateEmpty &&
           atomicCAS(reinterpret_cast<unsigned long long*>(state_ptr(a, s)), kStateEmpty, tag) ==
               kStateEmpty) {
         *reinterpret_cast<uint64_t*>(a.table + s * a.stride) = code;
-        lane_put_value(a, s, value, vals);
+        slot = s;
         return 1;
       }
     }
@@ -537,6 +561,7 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, cons
     if (base >= a.cap) base -= a.cap;
     if (left > 0) p = load_pair(a, base, left);
   }
+  slot = -1;
   return -1;
 }
 
@@ -934,86 +959,111 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   }
 }
 
-// One lane per query of the sub-call.
+// One lane per query of the sub-call; the wave then copies its answers' rows together.
 template <typename CodeT>
 __global__ __launch_bounds__(256) void bulk_query_kernel(StoreArgs a, BulkWs w) {
   constexpr int kParts = GtTraits<CodeT>::kParts;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t n = static_cast<int64_t>(a.n / a.T) * a.len;
-  if (i >= n) return;  // partition i / len, position i % len
-  const int64_t p = i / a.len;
-  const int o = static_cast<int>(i - p * a.len);
-  const int64_t base = p * a.T + a.s0;  // item of the sub-call's position 0
-  uint8_t* dst = a.out + (base + o) * a.vbytes;
-  int32_t j = w.src_in[i];
-  const CodeT code = static_cast<const CodeT*>(a.qc)[base + o];
-  if (j < 0) {
-    // the store's first read is in flight while the group table is consulted: most queries
-    // without an in-chunk answer end in the store
-    const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-    const int64_t h = home_slot(code, tag - 2, a.cap);
-    const PairHead first = load_pair(a, h, a.cap);
-    const uint64_t gh = splitmix_fin(code);
-    const int c = o / kChunk;
-    const int64_t pq = p * kParts + gt_part<CodeT>(gh);
-    uint32_t b1, b2;
-    gt_filter_bits(gh, b1, b2);
-    const uint32_t* f = w.filter + pq * kFilterWordsQ;
-    if (!((f[b1 >> 5] >> (b1 & 31)) & (f[b2 >> 5] >> (b2 & 31)) & 1u)) {
-      // no key of the sub-call has this code (no false negatives): the store
-    } else if (!w.spilled[pq]) {
-      const uint32_t m = gt_mask_of<CodeT>(w, p, code, gh) & ((1u << c) - 1u);
-      if (m) {
-        const int c2 = 31 - __clz(m);
-        const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
-        j = lp >= 0 ? c2 * kChunk + lp : -1;
-      }
-    } else {  // spilled part: the summaries of the earlier chunks, latest first
-      for (int c2 = c - 1; c2 >= 0 && j < 0; --c2) {
-        const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
-        if (lp >= 0) j = c2 * kChunk + lp;
-      }
-    }
+  uint8_t* dst = nullptr;  // stays null past the sub-call's queries
+  const uint8_t* src = nullptr;
+  if (i < n) {  // partition i / len, position i % len
+    const int64_t p = i / a.len;
+    const int o = static_cast<int>(i - p * a.len);
+    const int64_t base = p * a.T + a.s0;  // item of the sub-call's position 0
+    dst = a.out + (base + o) * a.vbytes;
+    int32_t j = w.src_in[i];
+    const CodeT code = static_cast<const CodeT*>(a.qc)[base + o];
     if (j < 0) {
-      const int64_t sl = lane_lookup(a, code, tag, h, first);
-      group_copy<1>(a, dst, sl >= 0 ? a.table + sl * a.stride + 16 : nullptr, 0);
-      return;
+      // the store's first read is in flight while the group table is consulted: most queries
+      // without an in-chunk answer end in the store
+      const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
+      const int64_t h = home_slot(code, tag - 2, a.cap);
+      const PairHead first = load_pair(a, h, a.cap);
+      const uint64_t gh = splitmix_fin(code);
+      const int c = o / kChunk;
+      const int64_t pq = p * kParts + gt_part<CodeT>(gh);
+      uint32_t b1, b2;
+      gt_filter_bits(gh, b1, b2);
+      const uint32_t* f = w.filter + pq * kFilterWordsQ;
+      if (!((f[b1 >> 5] >> (b1 & 31)) & (f[b2 >> 5] >> (b2 & 31)) & 1u)) {
+        // no key of the sub-call has this code (no false negatives): the store
+      } else if (!w.spilled[pq]) {
+        const uint32_t m = gt_mask_of<CodeT>(w, p, code, gh) & ((1u << c) - 1u);
+        if (m) {
+          const int c2 = 31 - __clz(m);
+          const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
+          j = lp >= 0 ? c2 * kChunk + lp : -1;
+        }
+      } else {  // spilled part: the summaries of the earlier chunks, latest first
+        for (int c2 = c - 1; c2 >= 0 && j < 0; --c2) {
+          const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
+          if (lp >= 0) j = c2 * kChunk + lp;
+        }
+      }
+      if (j < 0) {
+        const int64_t sl = lane_lookup(a, code, tag, h, first);
+        src = sl >= 0 ? a.table + sl * a.stride + 16 : nullptr;
+      }
     }
+    if (j >= 0) src = a.values + (base + j) * a.vbytes;
   }
-  group_copy<1>(a, dst, a.values + (base + j) * a.vbytes, 0);
+  wave_copy_rows(a, dst, src);
 }
 
 // The key of partition p with `code` at position lp of chunk c (its latest in the sub-call):
-// its value over the code's existing store entry, or into a claimed slot. The lookups of this
-// sub-call are over (previous kernel), and no other item looks for the same key, so the only
-// thing a concurrent claim can be mistaken for is code 0 (a claimed slot whose code is not
-// written yet reads as 0): code-0 keys wait for bulk_zero_kernel. Returns 1 for a claim.
-__device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, uint64_t code, int c,
-                                               int32_t lp) {
+// finds the code's existing store entry or claims a slot, and names the copy the caller makes,
+// `row` (the slot's value; null when the table is full) from `from` (the key's value). The
+// lookups of this sub-call are over (previous kernel), and no other item looks for the same
+// key, so the only thing a concurrent claim can be mistaken for is code 0 (a claimed slot
+// whose code is not written yet reads as 0): code-0 keys wait for bulk_zero_kernel. Returns 1
+// for a claim.
+__device__ __forceinline__ int bulk_place_key(const StoreArgs& a, int64_t p, uint64_t code, int c,
+                                              int32_t lp, uint8_t*& row, const uint8_t*& from) {
   const uint64_t tag = static_cast<uint64_t>(a.g0 + p) + 2;
-  const uint8_t* v = a.values + (p * a.T + a.s0 + c * kChunk + lp) * a.vbytes;
-  u32x4 vals[kSpecPieces];  // the value row, loaded with the first probe
-#pragma unroll
-  for (int k = 0; k < kSpecPieces; ++k)
-    vals[k] = a.spec && k < a.pieces ? *reinterpret_cast<const u32x4*>(v + 16 * k)
-                                     : u32x4{0u, 0u, 0u, 0u};
-  const int r = lane_insert(a, code, tag, v, vals, home_slot(code, tag - 2, a.cap));
+  from = a.values + (p * a.T + a.s0 + c * kChunk + lp) * a.vbytes;
+  int64_t s;
+  const int r = lane_insert(a, code, tag, home_slot(code, tag - 2, a.cap), s);
   if (r < 0) atomicOr(a.full, 1);
+  row = s >= 0 ? a.table + s * a.stride + 16 : nullptr;
   return r > 0 ? 1 : 0;
 }
 
+// bulk_place_key with the lane's own copy (for lanes that insert on their own).
+__device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, uint64_t code, int c,
+                                               int32_t lp) {
+  uint8_t* row;
+  const uint8_t* from;
+  const int r = bulk_place_key(a, p, code, c, lp, row, from);
+  if (row) group_copy<1>(a, row, from, 0);
+  return r;
+}
+
 // A code of the group table with its chunk mask: its latest key is in the highest chunk of
-// the mask.
+// the mask. Names the copy as bulk_place_key does (`row` null: nothing to copy).
 template <typename CodeT>
-__device__ __forceinline__ int bulk_insert_masked(const StoreArgs& a, const BulkWs& w, int64_t p,
-                                                  CodeT code, uint32_t mask) {
+__device__ __forceinline__ int bulk_place_masked(const StoreArgs& a, const BulkWs& w, int64_t p,
+                                                 CodeT code, uint32_t mask, uint8_t*& row,
+                                                 const uint8_t*& from) {
   const int c2 = 31 - __clz(mask);
   const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
   if (lp < 0) {  // the summary of a chunk in the mask holds the code; fail loudly
     atomicOr(a.full, 2);
+    row = nullptr;
     return 0;
   }
-  return bulk_insert_key(a, p, code, c2, lp);
+  return bulk_place_key(a, p, code, c2, lp, row, from);
+}
+
+// bulk_place_masked with the lane's own copy.
+template <typename CodeT>
+__device__ __forceinline__ int bulk_insert_masked(const StoreArgs& a, const BulkWs& w, int64_t p,
+                                                  CodeT code, uint32_t mask) {
+  uint8_t* row;
+  const uint8_t* from = nullptr;
+  const int r = bulk_place_masked<CodeT>(a, w, p, code, mask, row, from);
+  if (row) group_copy<1>(a, row, from, 0);
+  return r;
 }
 
 // One lane per entry of the group table; a workgroup's 256 entries lie in one part (parts are
@@ -1036,19 +1086,24 @@ __global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w)
   if (threadIdx.x == 0) n_claims = 0;
   __syncthreads();
   int claimed = 0;
-  if (!w.spilled[p * kParts + qt]) {
+  if (!w.spilled[p * kParts + qt]) {  // the same for the whole workgroup
+    uint8_t* row = nullptr;
+    const uint8_t* from = nullptr;
     if constexpr (sizeof(CodeT) == 4) {
       const unsigned long long word = w.gt[g];
       if (word != 0 && gt_code(word) != 0)
-        claimed = bulk_insert_masked<CodeT>(a, w, p, gt_code(word), static_cast<uint32_t>(word >> 32));
+        claimed = bulk_place_masked<CodeT>(a, w, p, gt_code(word), static_cast<uint32_t>(word >> 32),
+                                           row, from);
     } else {
       const CodeT code = w.gt[g];
-      if (code != SENT && code != 0) claimed = bulk_insert_masked<CodeT>(a, w, p, code, w.gmask[g]);
+      if (code != SENT && code != 0)
+        claimed = bulk_place_masked<CodeT>(a, w, p, code, w.gmask[g], row, from);
       if (in_q == 0 && gt_part<CodeT>(splitmix_fin(SENT)) == qt) {
         const uint32_t m = w.smask[p * kParts + qt];
         if (m) claimed += bulk_insert_masked<CodeT>(a, w, p, SENT, m);
       }
     }
+    wave_copy_rows(a, row, from);
   } else {
     const int per_chunk = kSlots + 1;
     for (int64_t q = in_q; q < static_cast<int64_t>(w.nch) * per_chunk; q += w.sub) {
@@ -1165,9 +1220,20 @@ using namespace lema;
 
 namespace {
 
-constexpr int64_t kBulkMinT = 2 * kChunk;  // longer calls take the bulk path
-
-bool bulk_applies(int64_t T) { return T > kBulkMinT; }
+// Bulk or chunked, by partitions P and positions T per call. A chunked launch runs one
+// workgroup per partition, so with few partitions most of the chip idles through the T/1024
+// launches in order, while the bulk kernels' costs per sub-call and per partition only pay
+// off over long enough calls. Measured on one MI355X (64-bit codes, 48- and 128-byte value
+// rows, microseconds chunked / bulk): T = 1024 is a tie or a loss for bulk at any P (24: 42 /
+// 49; 1024: 166 / 322); T = 2048 wins from 24 to 128 partitions (24: 85 / 56; 128: 109 / 100)
+// and loses from 256 (256: 115 / 147); T = 4096 wins up to 256 partitions (256: 272 / 252)
+// and loses at 1024 (740 / 872); T = 16384 wins everywhere (1024: 3169 / 3011).
+bool bulk_applies(int64_t P, int64_t T) {
+  if (T <= 1024) return false;
+  if (P <= 128) return true;
+  if (P >= 512) return T > 4096;
+  return T > 2048;
+}
 
 template <typename CodeT>
 int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
@@ -1257,6 +1323,8 @@ int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, con
   a.pieces = static_cast<int32_t>(vbytes / a.piece);
   a.pre = p16 && a.pieces <= kStepGroup;
   a.spec = p16 && a.pieces <= kSpecPieces;
+  a.cg_log2 = 0;
+  while ((1 << a.cg_log2) < a.pieces && a.cg_log2 < 4) ++a.cg_log2;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = n / T;
   if (T == 1) {
@@ -1267,7 +1335,7 @@ int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, con
     return launch_status("store_step_kernel");
   }
   LEMA_REQUIRE(P < (int64_t(1) << 31), "too many partitions (%lld)", (long long)P);
-  if (workspace != nullptr && bulk_applies(T)) {
+  if (workspace != nullptr && bulk_applies(P, T)) {
     LEMA_REQUIRE(P < (int64_t(1) << 31) - 1 && P * (T < kBulkSpan ? T : kBulkSpan) < (int64_t(1) << 31),
                  "too many items per sub-call (%lld partitions)", (long long)P);
     return code_bytes == 4 ? run_bulk<uint32_t>(a, workspace, ws_bytes, st)
@@ -1296,7 +1364,8 @@ extern "C" int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, con
 }
 
 extern "C" int64_t lema_store_workspace_bytes(int64_t n, int64_t T, int32_t code_bytes) {
-  if (T <= 0 || n <= 0 || n % T != 0 || (code_bytes != 4 && code_bytes != 8) || !bulk_applies(T))
+  if (T <= 0 || n <= 0 || n % T != 0 || (code_bytes != 4 && code_bytes != 8) ||
+      !bulk_applies(n / T, T))
     return 0;
   return bulk_layout(n / T, T, code_bytes).bytes;
 }

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from latest_exact_match_attention_amd import lema_from_codes
+from latest_exact_match_attention_amd import _lib, lema_from_codes
 from latest_exact_match_attention_amd.cache import HashStore, LemaCache
 
 pytestmark = pytest.mark.gpu
@@ -81,7 +81,16 @@ def test_store_one_shot(dev):
 
 
 def test_store_long_call_spans_subchunks(dev):
-    """T = 2500 per call: three 1024-position sub-chunks in order within one exchange."""
+    """T = 2500 per call over 600 partitions: the chunked path, three 1024-position sub-chunks
+    in order within one exchange."""
+    assert _lib.lib().lema_store_workspace_bytes(600 * 2500, 2500, 4) == 0
+    run_dict_case(dev, seed=5, P=600, T=2500, chunk=2500, n_codes=60, capacity=120_000,
+                  code_dtype=torch.int32)
+
+
+def test_store_short_long_call_few_partitions(dev):
+    """T = 2500 over 30 partitions takes the bulk path (one sub-call of three chunks)."""
+    assert _lib.lib().lema_store_workspace_bytes(30 * 2500, 2500, 4) > 0
     run_dict_case(dev, seed=5, P=30, T=2500, chunk=2500, n_codes=60, capacity=6000,
                   code_dtype=torch.int32)
 
@@ -412,18 +421,19 @@ def test_bulk_equals_chunked_path_and_insert_only(dev):
 
 
 def test_bulk_many_partitions_equals_chunked_path(dev):
-    """4,200 partitions x T = 2,100 (4,200 group tables, each partition's claims tallied from
+    """2,100 partitions x T = 4,200 (2,100 group tables, each partition's claims tallied from
     its workgroups): the bulk path (int32 and int64 codes) and the chunked path agree on
     outputs, entries and per-partition counts."""
     rng = np.random.default_rng(16)
-    P, T, cap = 4200, 2100, 9_000_000
+    P, T, cap = 2100, 4200, 9_000_000
+    assert _lib.lib().lema_store_workspace_bytes(P * T, T, 8) > 0
     qc = rng.integers(0, 700, size=P * T)
     kc = rng.integers(0, 700, size=P * T)
     v = torch.from_numpy(rng.integers(-30000, 30000, size=(P * T, D_V), dtype=np.int16)).to(dev)
     outs, dumps, counts = [], [], []
     for out, st in _three_paths(dev, qc, kc, v, P, T, cap):
         g, c, val = st.dump()
-        key = g * 1024 + c                                   # codes < 700, groups < 4200
+        key = g * 1024 + c                                   # codes < 700, groups < 2100
         order = torch.argsort(key)
         dumps.append((key[order], val[order]))
         outs.append(out)
