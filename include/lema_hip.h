@@ -190,6 +190,16 @@ int lema_skinny_swiglu_bf16(const void* x, int64_t ldx, const void* wg, const vo
                             int64_t ldw, int64_t M, int64_t N, int64_t K, void* out,
                             void* stream);
 
+/* The MLP input of a decode step and its gate and up products in one launch
+ * (code/lema/model.py:229-232, 85-94): s = x + d (each sum rounded to bf16; d NULL: s = x),
+ * h = bf16(s * rsqrt(mean(s^2) + eps) * nw) rounded exactly as lema_rmsnorm_bf16 rounds it,
+ * and out = lema_skinny_swiglu_bf16 of h; x_out receives s when d is given (a buffer apart
+ * from x and d). x, d, x_out: [M, K] bf16 rows, 16-byte aligned; M <= 32, K <= 2048, and
+ * M * (K + 8) * 2 bytes plus the partial sums within a workgroup's 160 KB of LDS. */
+int lema_skinny_norm_swiglu_bf16(const void* x, const void* d, const void* nw, float eps,
+                                 void* x_out, const void* wg, const void* wu, int64_t ldw,
+                                 int64_t M, int64_t N, int64_t K, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

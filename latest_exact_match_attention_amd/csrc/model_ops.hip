@@ -9,6 +9,7 @@
 //               of the row (online max and rescaled sum), instead of a fp32 copy plus a
 //               softmax pass.
 #include "lema_internal.h"
+#include "norm_row.h"
 
 namespace lema {
 namespace {
@@ -44,66 +45,20 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const u32x4* gate, const u3
   }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-// One wavefront per row of D bf16 (D % 8 == 0), 8 elements per lane per step.
-constexpr int kNormMaxSteps = 8;  // D <= 64 lanes * 8 * 8 = 4096
+// One wavefront per row of D bf16 (D % 8 == 0, D <= 512 * S).
+template <int S>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* d,
                                                       const uint16_t* w, float eps, int64_t rows,
                                                       int D, uint16_t* x_out, uint16_t* h_out) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int steps = D / 512 + (D % 512 ? 1 : 0);
-  u32x4 xv[kNormMaxSteps];
-  float ss = 0.0f;
-#pragma unroll
-  for (int s = 0; s < kNormMaxSteps; ++s) {
-    const int e = (s * 64 + lane) * 8;
-    if (s >= steps || e >= D) continue;
-    u32x4 v = *reinterpret_cast<const u32x4*>(x + row * D + e);
-    if (d != nullptr) {
-      const u32x4 dv = *reinterpret_cast<const u32x4*>(d + row * D + e);
-      uint32_t* pv = reinterpret_cast<uint32_t*>(&v);
-      const uint32_t* pd = reinterpret_cast<const uint32_t*>(&dv);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = f32_to_bf16(bf16_to_f32(pv[k] & 0xFFFFu) + bf16_to_f32(pd[k] & 0xFFFFu));
-        const uint32_t hi = f32_to_bf16(bf16_to_f32(pv[k] >> 16) + bf16_to_f32(pd[k] >> 16));
-        pv[k] = lo | (hi << 16);
-      }
-      *reinterpret_cast<u32x4*>(x_out + row * D + e) = v;
-    }
-    xv[s] = v;
-    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&v);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float a = bf16_to_f32(pv[k] & 0xFFFFu), b = bf16_to_f32(pv[k] >> 16);
-      ss += a * a + b * b;
-    }
-  }
-  const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
-#pragma unroll
-  for (int s = 0; s < kNormMaxSteps; ++s) {
-    const int e = (s * 64 + lane) * 8;
-    if (s >= steps || e >= D) continue;
-    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + e);
-    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&xv[s]);
-    const uint32_t* pw = reinterpret_cast<const uint32_t*>(&wv);
-    u32x4 o;
-    uint32_t* po = reinterpret_cast<uint32_t*>(&o);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = f32_to_bf16(bf16_to_f32(pv[k] & 0xFFFFu) * rstd * bf16_to_f32(pw[k] & 0xFFFFu));
-      const uint32_t hi = f32_to_bf16(bf16_to_f32(pv[k] >> 16) * rstd * bf16_to_f32(pw[k] >> 16));
-      po[k] = lo | (hi << 16);
-    }
-    *reinterpret_cast<u32x4*>(h_out + row * D + e) = o;
-  }
+  uint16_t* h = h_out + row * D;
+  const uint16_t* const xr[1] = {x + row * D};
+  const uint16_t* const dr[1] = {d != nullptr ? d + row * D : nullptr};
+  uint16_t* const sr[1] = {d != nullptr ? x_out + row * D : nullptr};
+  norm_rows<1, S>(xr, dr, 1, w, eps, D, lane, sr,
+               [h](int, int e, u32x4 v) { *reinterpret_cast<u32x4*>(h + e) = v; });
 }
 
 // One workgroup (256 threads) per row of V bf16 logits (V % 8 == 0, rows 16-byte aligned):
@@ -191,7 +146,9 @@ extern "C" int lema_rmsnorm_bf16(const void* x, const void* d, const void* w, fl
                "pointers must be 16-byte aligned");
   const int64_t grid = (rows + 3) / 4;
   LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows");
-  rmsnorm_kernel<<<dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+  // rows of up to 2048 (the models' widths) hold 4 steps in registers, longer ones 8
+  auto kernel = D <= 2048 ? rmsnorm_kernel<4> : rmsnorm_kernel<kNormMaxSteps>;
+  kernel<<<dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d),
       static_cast<const uint16_t*>(w), eps, rows, static_cast<int>(D),
       static_cast<uint16_t*>(x_out), static_cast<uint16_t*>(h_out));

@@ -16,11 +16,16 @@
 //           writes the bytes of each code its columns hold (d a multiple of 8), or whole heads;
 //   swiglu  silu(x . gate^T) * (x . up^T) with the same bf16 roundings as SwiGLU.forward's
 //           ops (code/lema/model.py:85-94): the block computes 16 columns of both.
+// A swiglu launch can also take the MLP's pre-norm (Block.forward's norm2 with the attention's
+// residual add, code/lema/model.py:229-232): every block then forms the normalised rows
+// itself, with the stand-alone norm kernel's arithmetic (norm_row.h), into LDS and multiplies
+// those; block 0 also writes x + d, the MLP's residual. That saves the norm's launch.
 //
 // Operand layout of v_mfma_f32_16x16x32_bf16 (checked on the device): lane l holds A row l%16
 // and B column l%16, k = 8 * (l / 16) + j, j < 8; the result's register r of lane l is row
 // 4 * (l / 16) + r, column l % 16.
 #include "lema_internal.h"
+#include "norm_row.h"
 
 namespace lema {
 namespace {
@@ -31,6 +36,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSkThreads = 512;
 constexpr int kSkWaves = kSkThreads / 64;
 constexpr int kSkUnroll = 4;  // K-steps of 32 with loads in flight per wavefront
+constexpr int kSkNormSteps = 4;  // a fused pre-norm's rows: up to 4 * 512 elements in registers
 
 // One weight segment of a launch: its blocks cover N output columns of x . w^T with one
 // epilogue. A launch holds up to three segments sharing x (the q, k and v projections of a
@@ -62,6 +68,12 @@ struct SkinnyArgs {
   int32_t d, T;  // pack: bits per code (one head), positions per stream (row m = (b, t))
   int32_t nseg;
   SkSegment seg[3];
+  // fused pre-norm (nw non-null): x is the residual stream, nd the addend (or null), rows of
+  // K; the product's input is norm(x + nd) * nw, and ns receives x + nd (rows of K)
+  const uint16_t* nd;
+  const uint16_t* nw;
+  uint16_t* ns;
+  float eps;
 };
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
@@ -78,9 +90,10 @@ __device__ __forceinline__ bool bf16_nonneg(float z) {
 
 // A block owns `cols` columns: 16 * CT, or 8 for a narrow plain segment (swiglu: 16 columns
 // of the gate and the same 16 of up).
-template <int MT, int CT>
+template <int MT, int CT, bool kNorm>
 __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   __shared__ float part[kSkWaves][MT * 16][CT * 16 + 1];
+  extern __shared__ __align__(16) uint16_t xs[];  // kNorm: the normalised rows, stride K + 8
   int bid = blockIdx.x, si = 0;
   while (si + 1 < a.nseg && bid >= a.seg[si].blocks) {
     bid -= a.seg[si].blocks;
@@ -109,11 +122,40 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
   }
   const uint16_t* xp[MT];
   bool xok[MT];
+  if constexpr (kNorm) {
+    // rows m and m + 8 of x by wavefront m, into LDS (a stride of K + 8 puts the 16 rows a
+    // fragment load reads in different banks)
+    const int xst = a.K + 8;
+    for (int m = wave; m < a.M; m += 2 * kSkWaves) {
+      const int n = m + kSkWaves < a.M ? 2 : 1;
+      const uint16_t* xr[2];
+      const uint16_t* dr[2];
+      uint16_t* sr[2];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * mt + r16;
-    xok[mt] = m < a.M;
-    xp[mt] = a.x + static_cast<int64_t>(xok[mt] ? m : 0) * a.ldx + kg;
+      for (int r = 0; r < 2; ++r) {
+        const int64_t mr = m + r * kSkWaves < a.M ? m + r * kSkWaves : m;
+        xr[r] = a.x + mr * a.ldx;
+        dr[r] = a.nd != nullptr ? a.nd + mr * a.K : nullptr;
+        sr[r] = blockIdx.x == 0 ? a.ns + mr * a.K : nullptr;
+      }
+      norm_rows<2, kSkNormSteps>(xr, dr, n, a.nw, a.eps, a.K, l, sr, [&](int r, int e, u32x4 h) {
+        *reinterpret_cast<u32x4*>(xs + (m + r * kSkWaves) * xst + e) = h;
+      });
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r16;
+      xok[mt] = m < a.M;
+      xp[mt] = xs + (xok[mt] ? m : 0) * xst + kg;
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r16;
+      xok[mt] = m < a.M;
+      xp[mt] = a.x + static_cast<int64_t>(xok[mt] ? m : 0) * a.ldx + kg;
+    }
   }
 
   f32x4 acc[MT][CT];
@@ -242,10 +284,17 @@ int launch_skinny(SkinnyArgs& a, hipStream_t st) {
     blocks += sg.blocks;
   }
   const dim3 grid(blocks), block(kSkThreads);
-  if (a.M <= 16)
-    skinny_kernel<1, CT><<<grid, block, 0, st>>>(a);
-  else
-    skinny_kernel<2, CT><<<grid, block, 0, st>>>(a);
+  if (a.nw != nullptr) {  // the normalised rows in LDS (checked to fit by the entry point)
+    const size_t lds = static_cast<size_t>(a.M) * (a.K + 8) * sizeof(uint16_t);
+    if (a.M <= 16)
+      skinny_kernel<1, CT, true><<<grid, block, lds, st>>>(a);
+    else
+      skinny_kernel<2, CT, true><<<grid, block, lds, st>>>(a);
+  } else if (a.M <= 16) {
+    skinny_kernel<1, CT, false><<<grid, block, 0, st>>>(a);
+  } else {
+    skinny_kernel<2, CT, false><<<grid, block, 0, st>>>(a);
+  }
   return launch_status("skinny_kernel");
 }
 
@@ -411,5 +460,40 @@ extern "C" int lema_skinny_swiglu_bf16(const void* x, int64_t ldx, const void* w
   a.nseg = 1;
   a.seg[0] = SkSegment{static_cast<const uint16_t*>(wg), static_cast<const uint16_t*>(wu), out,
                        nullptr, N, static_cast<int32_t>(N), kSkSwiglu, 0, 0};
+  return launch_ct(a, 2, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lema_skinny_norm_swiglu_bf16(const void* x, const void* d, const void* nw,
+                                            float eps, void* x_out, const void* wg,
+                                            const void* wu, int64_t ldw, int64_t M, int64_t N,
+                                            int64_t K, void* out, void* stream) {
+  clear_error();
+  if (int rc = check_skinny(x, K, ldw, M, K)) return rc;
+  if (int rc = check_weight(wg, N)) return rc;
+  if (int rc = check_weight(wu, N)) return rc;
+  LEMA_REQUIRE(out != nullptr, "bad output pointer");
+  LEMA_REQUIRE(K <= 512 * kSkNormSteps, "the fused norm takes rows of at most %d elements, got K=%lld",
+               512 * kSkNormSteps, (long long)K);
+  // LDS: the rows (M x (K + 8) bf16) next to the partial sums (8 x 16 or 32 rows x 33 floats)
+  const int64_t lds = M * (K + 8) * 2 + kSkWaves * (M <= 16 ? 16 : 32) * 33 * 4;
+  LEMA_REQUIRE(lds <= 160 * 1024, "%lld rows of %lld do not fit the LDS of a workgroup",
+               (long long)M, (long long)K);
+  LEMA_REQUIRE(nw != nullptr && aligned(nw, 16), "norm weight must be a 16-byte aligned device pointer");
+  LEMA_REQUIRE(d == nullptr || (aligned(d, 16) && x_out != nullptr && aligned(x_out, 16) &&
+                                x_out != x && x_out != d),
+               "the addend needs a 16-byte aligned output for x + d that is neither input");
+  SkinnyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = K;
+  a.ldw = ldw;
+  a.M = static_cast<int32_t>(M);
+  a.K = static_cast<int32_t>(K);
+  a.nseg = 1;
+  a.seg[0] = SkSegment{static_cast<const uint16_t*>(wg), static_cast<const uint16_t*>(wu), out,
+                       nullptr, N, static_cast<int32_t>(N), kSkSwiglu, 0, 0};
+  a.nd = static_cast<const uint16_t*>(d);
+  a.nw = static_cast<const uint16_t*>(nw);
+  a.ns = static_cast<uint16_t*>(x_out);
+  a.eps = eps;
   return launch_ct(a, 2, static_cast<hipStream_t>(stream));
 }

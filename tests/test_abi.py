@@ -44,6 +44,15 @@ def test_host_validation_statuses(L):
                        None) == _lib.BAD_ARG
     assert L.lema_gather(None, 2, 1, 1, 1, 1, 0, 0, 0, None, 5, None, 0, 0, 0, 0,
                          None) == _lib.BAD_ARG
+    # the MLP launch with its pre-norm: x, d, nw, eps, x_out, wg, wu, ldw, M, N, K, out, stream
+    f = L.lema_skinny_norm_swiglu_bf16
+    assert f(256, 512, 768, 1e-5, 1024, 1280, 1536, 64, 33, 64, 64, 1792, None) == _lib.BAD_ARG
+    assert f(256, 512, 768, 1e-5, 256, 1280, 1536, 64, 4, 64, 64, 1792, None) == _lib.BAD_ARG
+    assert b"neither input" in L.lema_last_error()
+    assert f(256, 512, 768, 1e-5, 1024, 1280, 1536, 2080, 4, 64, 2080, 1792, None) == _lib.BAD_ARG
+    assert b"at most 2048" in L.lema_last_error()
+    assert f(256, 512, 768, 1e-5, 1024, 1280, 1536, 2048, 32, 64, 2048, 1792, None) == _lib.BAD_ARG
+    assert b"LDS" in L.lema_last_error()
     # empty work is a no-op that touches no pointer
     assert L.lema_latest_prev_match(None, None, 8, 0, 5, None, 8, None) == _lib.OK
     assert L.lema_pack_codes(None, 2, 0, 4, 4, 8, 0, 0, 0, None, 8, None) == _lib.OK

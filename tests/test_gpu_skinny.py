@@ -131,3 +131,60 @@ def test_skinny_gemm_add_residual(dev, M, N, K):
     _lib.check(fn(x.data_ptr(), K, w.data_ptr(), K, r.data_ptr(), r.data_ptr(), N, M, N, K,
                   _lib.stream_of(x)))
     assert torch.equal(r.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("with_d", [True, False])
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(6144, 1536), (40, 64), (1024, 2048)])
+def test_skinny_norm_swiglu_equals_unfused(dev, M, N, K, with_d):
+    """The MLP's pre-norm inside the gate/up launch against the norm kernel followed by the
+    unfused launch, bit for bit (the normalised rows and x + d round alike). Rows that do not
+    fit a workgroup's LDS (32 of 2048) are refused on the host."""
+    from latest_exact_match_attention_amd.model import rms_norm
+    g = torch.Generator(device=dev).manual_seed(M * 3 + N + K)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    d = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16) if with_d else None
+    norm = torch.nn.RMSNorm(K, eps=1e-5).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(K, device=dev, generator=g))
+    wg, wu = ((torch.randn(N, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+              for _ in range(2))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    xo = torch.full_like(x, 7.0)
+    args = (x.data_ptr(), d.data_ptr() if d is not None else None, norm.weight.data_ptr(), 1e-5,
+            xo.data_ptr(), wg.data_ptr(), wu.data_ptr(), K, M, N, K, out.data_ptr(),
+            _lib.stream_of(x))
+    if M * (K + 8) * 2 + 8 * (16 if M <= 16 else 32) * 33 * 4 > 160 * 1024:
+        with pytest.raises(Exception, match="LDS"):
+            _lib.check(_lib.lib().lema_skinny_norm_swiglu_bf16(*args))
+        return
+    _lib.check(_lib.lib().lema_skinny_norm_swiglu_bf16(*args))
+    with torch.no_grad():
+        h, s = rms_norm(x, norm, d)
+    want = torch.empty_like(out)
+    _lib.check(_lib.lib().lema_skinny_swiglu_bf16(h.data_ptr(), K, wg.data_ptr(), wu.data_ptr(),
+                                                  K, M, N, K, want.data_ptr(), _lib.stream_of(x)))
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    if with_d:
+        assert torch.equal(xo.view(torch.int16), s.view(torch.int16))
+    else:
+        assert (xo == 7.0).all()                      # no addend: x_out is left alone
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_block_mlp_half_fused_equals_unfused(dev, B):
+    """Block.forward's MLP half on a decode step: SwiGLU.forward_normed (norm inside the
+    gate/up launch) returns what rms_norm followed by SwiGLU.forward returns, bit for bit."""
+    from latest_exact_match_attention_amd.model import SwiGLU, rms_norm
+    torch.manual_seed(B)
+    mlp = SwiGLU(1536, 4096).to(dev, torch.bfloat16)
+    norm = torch.nn.RMSNorm(1536, eps=1e-5).to(dev, torch.bfloat16)
+    x = torch.randn(B, 1, 1536, device=dev).to(torch.bfloat16)
+    d = torch.randn(B, 1, 1536, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(1536, device=dev))
+        got = mlp.forward_normed(x, d, norm)
+        h, s = rms_norm(x, norm, d)
+        want = mlp(h, residual=s)
+    assert got is not None
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
