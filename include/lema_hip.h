@@ -150,6 +150,18 @@ int lema_rmsnorm_bf16(const void* x, const void* d, const void* w, float eps, in
 int lema_cross_entropy_bf16(const void* logits, int64_t rows, int64_t V, int64_t ld,
                             const int64_t* target, float* loss, void* stream);
 
+/* out[r * out_stride] = argmax of row r of bf16 values (V and the row stride ld multiples of
+ * 8): the first index of the maximum, NaN above every number, as torch.argmax. Replaces the
+ * greedy pick of code/lema/decode.py:71-93 (logits.argmax(-1)), written straight into a
+ * token buffer. */
+int lema_argmax_bf16(const void* x, int64_t rows, int64_t V, int64_t ld, int64_t* out,
+                     int64_t out_stride, void* stream);
+
+/* out row i = table row ids[i] of D bf16 (D % 8 == 0), zeros for an id outside [0, vocab):
+ * the token embedding of a decode step (nn.Embedding, code/lema/model.py's tok_emb). */
+int lema_embedding_bf16(const void* table, int64_t vocab, int64_t D, const int64_t* ids,
+                        int64_t n, void* out, void* stream);
+
 /* ---- decode-shaped products on the matrix cores (bf16, fp32 accumulation) ---- */
 
 /* y[M, N] = x[M, K] . w[N, K]^T rounded to bf16, for 1 <= M <= 32 rows (a decode step's

@@ -45,6 +45,8 @@ PROTOTYPES = {
     "lema_store_workspace_bytes": ([_i64, _i64, _i32], ctypes.c_int64),
     "lema_swiglu_bf16": ([_p, _p, _p, _i64, _p], ctypes.c_int),
     "lema_rmsnorm_bf16": ([_p, _p, _p, ctypes.c_float, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "lema_argmax_bf16": ([_p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),
+    "lema_embedding_bf16": ([_p, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
     "lema_cross_entropy_bf16": ([_p, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "lema_skinny_gemm_bf16": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
     "lema_skinny_pack_bf16": ([_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _i64, _p, _i32, _p],

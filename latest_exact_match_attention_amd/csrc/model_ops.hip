@@ -7,7 +7,9 @@
 //               x_out^2) + eps) * w (Block's pre-norms, the final norm);
 //   xent        per row, logsumexp(logits) - logits[target] from bf16 logits in fp32, one read
 //               of the row (online max and rescaled sum), instead of a fp32 copy plus a
-//               softmax pass.
+//               softmax pass;
+//   argmax      a decode step's greedy pick, written straight into the token buffer;
+//   embedding   the token embedding rows of a decode step, one workgroup per row.
 #include "lema_internal.h"
 #include "norm_row.h"
 
@@ -155,6 +157,75 @@ extern "C" int lema_rmsnorm_bf16(const void* x, const void* d, const void* w, fl
   return launch_status("rmsnorm_kernel");
 }
 
+// Is (a, ia) ahead of (b, ib) for torch.argmax: NaN above every number, then the larger value,
+// then the lower index.
+__device__ __forceinline__ bool argmax_ahead(float a, int64_t ia, float b, int64_t ib) {
+  const bool an = a != a, bn = b != b;
+  if (an || bn) return an && (!bn || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+// One workgroup (1024 threads) per row of V bf16 values (V % 8 == 0, rows 16-byte aligned):
+// out[row * out_stride] = the row's argmax (code/lema/decode.py:71-93, the greedy pick).
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* x, int64_t V, int64_t ld,
+                                                      int64_t* out, int64_t out_stride) {
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
+  const int64_t row = blockIdx.x;
+  const uint16_t* r = x + row * ld;
+  float bv = 0.0f;
+  int64_t bi = -1;  // none yet
+  for (int64_t e = static_cast<int64_t>(threadIdx.x) * 8; e < V; e += 1024 * 8) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(r + e);
+    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float f = bf16_to_f32((pv[k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
+      if (bi < 0 || argmax_ahead(f, e + k, bv, bi)) {
+        bv = f;
+        bi = e + k;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int64_t oi = __shfl_xor(bi, o);
+    if (oi >= 0 && (bi < 0 || argmax_ahead(ov, oi, bv, bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (si[w] >= 0 && (bi < 0 || argmax_ahead(sv[w], si[w], bv, bi))) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    out[row * out_stride] = bi;
+  }
+}
+
+// One workgroup per id: out row i = table row ids[i] (D bf16, D % 8 == 0, 16-byte aligned
+// rows), or zeros for an id outside [0, vocab).
+__global__ __launch_bounds__(256) void embedding_kernel(const uint16_t* table, int64_t vocab,
+                                                        int64_t D, const int64_t* ids,
+                                                        uint16_t* out) {
+  const int64_t i = blockIdx.x;
+  const int64_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  const u32x4* src = reinterpret_cast<const u32x4*>(table + (ok ? id : 0) * D);
+  u32x4* dst = reinterpret_cast<u32x4*>(out + i * D);
+  for (int64_t k = threadIdx.x; k < D / 8; k += blockDim.x)
+    dst[k] = ok ? src[k] : u32x4{0u, 0u, 0u, 0u};
+}
+
 extern "C" int lema_cross_entropy_bf16(const void* logits, int64_t rows, int64_t V, int64_t ld,
                                        const int64_t* target, float* loss, void* stream) {
   clear_error();
@@ -168,4 +239,32 @@ extern "C" int lema_cross_entropy_bf16(const void* logits, int64_t rows, int64_t
   xent_kernel<<<dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(logits), V, ld, target, loss);
   return launch_status("xent_kernel");
+}
+
+extern "C" int lema_argmax_bf16(const void* x, int64_t rows, int64_t V, int64_t ld, int64_t* out,
+                                int64_t out_stride, void* stream) {
+  clear_error();
+  LEMA_REQUIRE(rows >= 0 && V > 0 && V % 8 == 0 && ld >= V && ld % 8 == 0,
+               "row length %lld and stride %lld must be multiples of 8", (long long)V,
+               (long long)ld);
+  if (rows == 0) return LEMA_OK;
+  LEMA_REQUIRE(x && out && aligned(x, 16) && aligned(out, 8) && out_stride >= 1, "bad pointer");
+  LEMA_REQUIRE(rows < (int64_t(1) << 31), "too many rows");
+  argmax_kernel<<<dim3(rows), dim3(1024), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(x), V, ld, out, out_stride);
+  return launch_status("argmax_kernel");
+}
+
+extern "C" int lema_embedding_bf16(const void* table, int64_t vocab, int64_t D, const int64_t* ids,
+                                   int64_t n, void* out, void* stream) {
+  clear_error();
+  LEMA_REQUIRE(vocab >= 1 && D > 0 && D % 8 == 0, "rows of %lld must be a multiple of 8",
+               (long long)D);
+  if (n == 0) return LEMA_OK;
+  LEMA_REQUIRE(n > 0 && n < (int64_t(1) << 31), "bad id count %lld", (long long)n);
+  LEMA_REQUIRE(table && ids && out && aligned(table, 16) && aligned(ids, 8) && aligned(out, 16),
+               "bad pointer");
+  embedding_kernel<<<dim3(n), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(table), vocab, D, ids, static_cast<uint16_t*>(out));
+  return launch_status("embedding_kernel");
 }

@@ -19,23 +19,23 @@ import contextlib
 import torch
 
 from .cache import HashStore, LemaCache
-from .model import linear, rms_norm
+from .model import argmax_into, embed, linear, rms_norm
 
 __all__ = ["LemaDecoder", "decoder", "worst_case_codes"]
 
 
 def _chooser(temperature: float):
-    """Logits -> next token: argmax, or a draw from softmax(logits / temperature) by the
-    Gumbel-max trick (code/lema/decode.py:71-93): argmax(logits / T + g) with g = -log(E),
-    E ~ Exponential(1). In fp32, so near-tied bf16 logits stay distinct. Inside a graph the
-    generator advances on every replay."""
+    """(logits, tok) -> next token written into tok: argmax, or a draw from
+    softmax(logits / temperature) by the Gumbel-max trick (code/lema/decode.py:71-93):
+    argmax(logits / T + g) with g = -log(E), E ~ Exponential(1). In fp32, so near-tied bf16
+    logits stay distinct. Inside a graph the generator advances on every replay."""
     if temperature <= 0:
-        return lambda logits: logits.argmax(-1)
+        return argmax_into
 
-    def pick(logits):
+    def pick(logits, tok):
         z = logits.float() / temperature
         g = torch.empty_like(z).exponential_().log().neg_()
-        return (z + g).argmax(-1)
+        tok.copy_((z + g).argmax(-1))
     return pick
 
 
@@ -72,18 +72,20 @@ class LemaDecoder:
         dev = next(model.parameters()).device
         self.tok = torch.zeros(B, 1, dtype=torch.long, device=dev)
         if tok is not None:
+            if bool(((tok < 0) | (tok >= cfg.vocab_size)).any()):
+                raise ValueError(f"tokens must lie in [0, {cfg.vocab_size})")
             self.tok.copy_(tok)
         views = [cache.layer(i) for i in range(L)]
         segs = [b.seg or (b.gpu_pre, b.gpu_post) for b in model.blocks]
         choose = _chooser(temperature)
 
         def step_fn():
-            x = model.tok_emb(self.tok)
+            x = embed(model.tok_emb, self.tok)
             for i in range(L):
                 qc, kc, v = segs[i][0](x)
                 x = segs[i][1](x, views[i].exchange(qc, kc, v, check=False))
             logits = linear(rms_norm(x, model.norm_f)[0], model.lm_head)
-            self.tok.copy_(choose(logits))
+            choose(logits, self.tok)
             return logits
 
         tok0 = self.tok.clone()

@@ -36,6 +36,7 @@ from . import _lib
 from .attention import code_dtype_for, lema_hard, pack_codes
 
 __all__ = ["ModelConfig", "SwiGLU", "Attention", "Block", "Transformer", "lm_loss", "rms_norm",
+           "embed", "argmax_into",
            "swiglu", "cross_entropy_sum"]
 
 # ------------------------------------------------------------------ fused bf16 segments
@@ -62,6 +63,33 @@ def rms_norm(x: torch.Tensor, norm: nn.RMSNorm, d: torch.Tensor | None = None):
         float(eps), x.numel() // D, D, xo.data_ptr() if d is not None else None, h.data_ptr(),
         _lib.stream_of(x)))
     return h, xo
+
+
+def embed(emb: nn.Embedding, ids: torch.Tensor) -> torch.Tensor:
+    """emb(ids) for a decode step: bf16 rows gathered by one workgroup each. The ids must lie
+    in [0, vocab) (an id outside it gives a zero row where nn.Embedding raises)."""
+    w = emb.weight
+    if not (_fused(w) and ids.is_cuda and ids.dtype == torch.long and ids.is_contiguous()
+            and w.shape[1] % 8 == 0 and w.data_ptr() % 16 == 0):
+        return emb(ids)
+    out = torch.empty(ids.shape + (w.shape[1],), dtype=w.dtype, device=w.device)
+    _lib.check(_lib.lib().lema_embedding_bf16(w.data_ptr(), w.shape[0], w.shape[1],
+                                              ids.data_ptr(), ids.numel(), out.data_ptr(),
+                                              _lib.stream_of(w)))
+    return out
+
+
+def argmax_into(logits: torch.Tensor, out: torch.Tensor) -> None:
+    """out[...] = logits.argmax(-1) (the first index of the maximum, NaN above every number),
+    written in place: one workgroup per row of bf16 logits."""
+    V = logits.shape[-1]
+    if not (_fused(logits) and V % 8 == 0 and logits.data_ptr() % 16 == 0 and out.is_cuda
+            and out.dtype == torch.long and out.is_contiguous()
+            and out.numel() == logits.numel() // V):
+        out.copy_(logits.argmax(-1).view(out.shape))
+        return
+    _lib.check(_lib.lib().lema_argmax_bf16(logits.data_ptr(), logits.numel() // V, V, V,
+                                           out.data_ptr(), 1, _lib.stream_of(logits)))
 
 
 def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:

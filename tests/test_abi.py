@@ -53,6 +53,8 @@ def test_host_validation_statuses(L):
     assert b"at most 2048" in L.lema_last_error()
     assert f(256, 512, 768, 1e-5, 1024, 1280, 1536, 2048, 32, 64, 2048, 1792, None) == _lib.BAD_ARG
     assert b"LDS" in L.lema_last_error()
+    assert L.lema_argmax_bf16(256, 2, 7, 8, 512, 1, None) == _lib.BAD_ARG
+    assert L.lema_embedding_bf16(256, 10, 12, 512, 3, 768, None) == _lib.BAD_ARG
     # empty work is a no-op that touches no pointer
     assert L.lema_latest_prev_match(None, None, 8, 0, 5, None, 8, None) == _lib.OK
     assert L.lema_pack_codes(None, 2, 0, 4, 4, 8, 0, 0, 0, None, 8, None) == _lib.OK

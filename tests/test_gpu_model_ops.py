@@ -52,3 +52,37 @@ def test_cross_entropy_from_bf16_logits(dev):
     got = cross_entropy_sum(logits, y)
     want = F.cross_entropy(logits.float(), y, reduction="sum")
     assert abs(got.item() - want.item()) <= 1e-5 * abs(want.item())
+
+
+@pytest.mark.parametrize("rows", [1, 16, 33])
+@pytest.mark.parametrize("V", [50304, 8, 64, 8200])
+def test_argmax_equals_torch(dev, rows, V):
+    """The decode step's greedy pick against torch.argmax on bf16 logits: planted ties (the
+    first index wins), NaNs (above every number, the first one wins) and all -inf rows."""
+    from latest_exact_match_attention_amd.model import argmax_into
+    g = torch.Generator(device=dev).manual_seed(rows * 7 + V)
+    x = torch.randn(rows, V, device=dev, generator=g).to(torch.bfloat16)
+    if V >= 64:
+        x[0, V // 3] = x[0, V - 5] = 9.0                      # a tie: the lower index
+        if rows > 1:
+            x[1, V - 1] = float("nan")                          # NaN wins
+            x[1, 5] = 100.0
+        if rows > 2:
+            x[2].fill_(float("-inf"))                           # all -inf: index 0
+            x[3 % rows, 7] = x[3 % rows, 3] = float("nan")      # the first NaN
+    out = torch.full((rows, 1), -9, dtype=torch.long, device=dev)
+    argmax_into(x.view(rows, 1, V), out)
+    assert torch.equal(out.view(-1), x.argmax(-1))
+
+
+def test_embedding_equals_torch(dev):
+    """Decode-step embedding rows against nn.Embedding bit for bit; ids outside the table give
+    zero rows (where nn.Embedding raises)."""
+    from latest_exact_match_attention_amd.model import embed
+    emb = torch.nn.Embedding(50304, 1536).to(dev, torch.bfloat16)
+    ids = torch.tensor([[0], [50303], [17], [17], [31000]], device=dev)
+    got = embed(emb, ids)
+    assert torch.equal(got.view(torch.int16), emb(ids).view(torch.int16))
+    bad = torch.tensor([[-1], [50304], [3]], device=dev)
+    got = embed(emb, bad)
+    assert (got[:2] == 0).all() and torch.equal(got[2], emb.weight[3].view(1, -1))
