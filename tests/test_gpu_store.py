@@ -335,10 +335,12 @@ def test_bulk_spilled_quarter(dev):
     store.check_full()
 
 
-@pytest.mark.parametrize("d_v", [32, 40, 64])
+@pytest.mark.parametrize("d_v", [4, 12, 20, 32, 40, 64, 144])
 def test_bulk_long_value_rows(dev, d_v):
-    """Rows of 64, 80 and 128 bytes through two long calls: up to four 16-byte pieces a key's
-    value row is held in registers while its slot is found, beyond that it is copied."""
+    """Rows of 8 to 288 bytes through two long calls. The wave copies the rows it names
+    together, each row by a power-of-two group of lanes: 8-byte pieces for rows of 8, 24 and
+    40 bytes (1, 3 and 5 pieces), 16-byte pieces for 64, 80 and 128 bytes, and 18 pieces over
+    16 lanes (two each) for 288 bytes."""
     run_store_rows_case(dev, seed=100 + d_v, d_v=d_v, P=3, Ts=(5000, 2600))
 
 
