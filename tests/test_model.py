@@ -142,3 +142,21 @@ def test_losses_run_the_head_as_plain_gemms():
     sd = {k: v.float() for k, v in Transformer(cfg).state_dict().items()}
     ops = _aten_ops(lambda: torch_model.loss(sd, cfg, x, y, chunk=32))
     assert "aten::bmm" not in ops
+
+
+def test_fused_decode_segments_decline_what_they_cannot_take():
+    """The MLP-with-pre-norm launch, the embedding gather and the argmax are device bf16 paths:
+    on CPU tensors forward_normed declines (the caller then runs rms_norm and the MLP), and the
+    embedding and argmax fall back to the torch ops they mirror."""
+    from latest_exact_match_attention_amd.model import SwiGLU, argmax_into, embed
+    mlp = SwiGLU(64, 128).to(torch.bfloat16)
+    norm = torch.nn.RMSNorm(64, eps=1e-5).to(torch.bfloat16)
+    x = torch.randn(2, 1, 64).to(torch.bfloat16)
+    assert mlp.forward_normed(x, x.clone(), norm) is None
+    emb = torch.nn.Embedding(10, 8)
+    ids = torch.tensor([[3], [9]])
+    assert torch.equal(embed(emb, ids), emb(ids))
+    logits = torch.tensor([[[0.5, 2.0, 2.0, -1.0]], [[float("nan"), 1.0, 3.0, 0.0]]])
+    tok = torch.zeros(2, 1, dtype=torch.long)
+    argmax_into(logits, tok)
+    assert tok.view(-1).tolist() == [1, 0]
