@@ -547,6 +547,11 @@ def bench_long(a):
         host_table = torch.zeros((cap_h, 16 + 2 * dv), dtype=torch.uint8)
         host_counts = torch.zeros(H, dtype=torch.int64)
     stream = torch.cuda.current_stream(dev)
+    if a.copy_probe:                     # one plain copy of 256 MiB: calibrates the counters
+        probe = torch.zeros(128 << 20, dtype=torch.int16, device=dev)
+        torch.empty_like(probe).copy_(probe)
+        torch.cuda.synchronize()
+        del probe
     total_ms, per_call, cpu_s, same = 0.0, [], [], True
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for c in range(calls):
@@ -610,7 +615,8 @@ def bench_long(a):
                    "table_bytes": cap * (16 + 2 * dv), "load_after": round(store.load(), 4),
                    "ms_per_call": per_call, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic("bulk_kernels/long_context"),
                      "kernel": "store exchange (all launches of a call)",
                      "bytes_per_query": bpq, "queries_per_call": H * L},
         "cpu_baseline": cpu,

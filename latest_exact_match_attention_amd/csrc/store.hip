@@ -571,17 +571,19 @@ __device__ int lane_insert(const StoreArgs& a, uint64_t code, uint64_t tag, int6
 // sub-chunk:
 //   chunks   one workgroup per (partition, 1024-chunk): in-chunk answers of the queries (LDS
 //            resolver), the chunk's key summary (code -> latest position, the LDS table
-//            written out), and its distinct key codes listed per part of the group table;
+//            written out), and its distinct key codes listed per part of the group table, each
+//            with its latest position;
 //   table    one workgroup per (partition, part of the code hash space): the part's codes of
 //            every chunk entered in an LDS table, code -> mask of the chunks holding keys with
-//            it, written out as that part of the partition's group table;
+//            it and the latest key of all of them, written out as that part of the
+//            partition's group table;
 //   queries  a query without an in-chunk answer takes the highest chunk below its own in its
 //            code's mask and that chunk's summary gives the key; with no such chunk it looks
 //            the store up (the table still holds exactly the keys before the sub-call);
-//   insert   every (partition, code) of the sub-call takes its latest key from the summary of
-//            the highest chunk in its mask and writes that value over its existing store entry
-//            or claims a slot (code 0 in a kernel of its own, see bulk_insert_kernel); the
-//            claims are counted per partition on the way.
+//   insert   every (partition, code) of the sub-call takes its latest key from its group-table
+//            entry and writes that value over its existing store entry or claims a slot (code
+//            0 in a kernel of its own, see bulk_insert_kernel); the claims are counted per
+//            partition on the way.
 // The kernel boundary orders every lookup of the sub-call before its inserts. A part with
 // more codes than its LDS table takes (only codes chosen to collide in the hash get there) is
 // marked spilled: its queries and inserts then search the chunk summaries themselves.
@@ -596,8 +598,9 @@ constexpr int kFilterWordsQ = (1 << kFilterBitsLog2) / 32;
 // Group table per partition: `cap` entries in kParts parts of `sub` entries; a code lives in the
 // part given by the top bits of its hash, at the slot given by the low bits, with linear
 // probing inside the part. Bit c of an entry's mask: chunk c of the sub-call holds keys with
-// the code.
-//   32-bit codes: 4 parts of up to 16,384 words; a word is code | mask << 32, 0 = free (an
+// the code; beside each entry, its code's latest key in the sub-call (a position below
+// kBulkSpan).
+//   32-bit codes: 8 parts of up to 8,192 words; a word is code | mask << 32, 0 = free (an
 //     entered word always has a mask bit set).
 //   64-bit codes: 8 parts of up to 8,192 entries; an entry is a code word (the all-ones code
 //     marks a free one) and a 32-bit mask word; the all-ones code's own mask is kept per
@@ -606,14 +609,19 @@ template <typename CodeT>
 struct GtTraits;
 template <>
 struct GtTraits<uint32_t> {
-  static constexpr int kParts = 4, kPartLog2 = 2, kPartMax = 16384;
+  static constexpr int kParts = 8, kPartLog2 = 3, kPartMax = 8192;
 };
 template <>
 struct GtTraits<uint64_t> {
   static constexpr int kParts = 8, kPartLog2 = 3, kPartMax = 8192;
 };
-static_assert(GtTraits<uint32_t>::kPartMax * 8 <= kTableLdsBytes, "LDS table");
-static_assert(GtTraits<uint64_t>::kPartMax * 12 <= kTableLdsBytes, "LDS table");
+// The table kernel's LDS: entries (8 bytes), masks (64-bit codes, 4 bytes) and latest
+// positions (4 bytes) of up to kPartMax codes, at fixed offsets for both code widths.
+constexpr int kLdsMaskOff = GtTraits<uint64_t>::kPartMax * 8;
+constexpr int kLdsPosOff = kLdsMaskOff + GtTraits<uint64_t>::kPartMax * 4;
+static_assert(GtTraits<uint32_t>::kPartMax == GtTraits<uint64_t>::kPartMax &&
+                  kLdsPosOff + GtTraits<uint64_t>::kPartMax * 4 <= kTableLdsBytes,
+              "LDS table");
 
 struct BulkWs {
   unsigned long long* gt;  // P x cap words: code | mask (32-bit codes) or codes (64-bit)
@@ -626,7 +634,10 @@ struct BulkWs {
   int32_t* src_in;         // per query of the sub-call: in-chunk answer (sub-call position) or -1
   void* qlist;             // per (partition, chunk, part): the chunk's distinct key codes of
                            // the part, up to kChunk
+  uint16_t* qlpos;         // beside qlist: each code's latest key as a sub-call position
   int32_t* qcount;         // per (partition, chunk, part): their number
+  uint32_t* gpos;          // P x cap: an entry's latest key of the sub-call (sub-call position)
+  uint32_t* spos;          // 64-bit codes: per (partition, part) the all-ones code's latest key
   uint32_t* claims;        // per workgroup of bulk_insert_kernel: store slots it claimed
   uint32_t* filter;        // per (partition, part): kFilterWordsQ words, two bits set per key
                            // code of the sub-call (gt_filter_bits)
@@ -780,15 +791,19 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
   const int lane = t & 63;
   const unsigned long long below = (1ull << lane) - 1;
   CodeT* lists = static_cast<CodeT*>(w.qlist) + sum * kParts * kChunk;
+  uint16_t* lpos = w.qlpos + sum * kParts * kChunk;
   constexpr int kRounds = (kSlots + 1 + kThreads - 1) / kThreads;
   CodeT rc[kRounds];
   int rq[kRounds];  // the slot's part, or -1 when the chunk holds no key with its code
+  uint16_t rp[kRounds];  // the code's latest key as a sub-call position (< kBulkSpan)
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int x = r * kThreads + t;
     rc[r] = x < kSlots ? s.code[x] : SENT;
-    const bool held = x < kSlots ? rc[r] != SENT : x == kSlots && s.pos[kSlots] >= 0;
+    const int lp = x <= kSlots ? s.pos[x] : -1;
+    const bool held = x < kSlots ? rc[r] != SENT : x == kSlots && lp >= 0;
     rq[r] = held ? gt_part<CodeT>(splitmix_fin(rc[r])) : -1;
+    rp[r] = static_cast<uint16_t>(held ? c * kChunk + lp : 0);
   }
 #pragma unroll
   for (int qq = 0; qq < kParts; ++qq) {
@@ -805,7 +820,11 @@ __global__ __launch_bounds__(kThreads) void bulk_chunk_kernel(StoreArgs a, BulkW
     at = __shfl(at, 0);
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
-      if (rq[r] == qq) lists[qq * kChunk + at + __popcll(bal[r] & below)] = rc[r];
+      if (rq[r] == qq) {
+        const int i = qq * kChunk + at + __popcll(bal[r] & below);
+        lists[i] = rc[r];
+        lpos[i] = rp[r];
+      }
       at += __popcll(bal[r]);
     }
   }
@@ -839,9 +858,10 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   __shared__ uint32_t bits[kFilterWordsQ];
   __shared__ int32_t start[kBulkSpan / kChunk + 1];  // the part's codes before chunk c
   __shared__ int32_t n_codes, zero_at;
-  __shared__ uint32_t sent_mask;
+  __shared__ uint32_t sent_mask, sent_pos;
   unsigned long long* tab = reinterpret_cast<unsigned long long*>(lds);  // words or codes
-  uint32_t* masks = reinterpret_cast<uint32_t*>(lds + GtTraits<uint64_t>::kPartMax * 8);
+  uint32_t* masks = reinterpret_cast<uint32_t*>(lds + kLdsMaskOff);
+  uint32_t* lposs = reinterpret_cast<uint32_t*>(lds + kLdsPosOff);  // latest key per entry
   const CodeT SENT = sentinel<CodeT>();
   const int64_t p = blockIdx.x / kParts;
   const int qt = static_cast<int>(blockIdx.x % kParts);
@@ -855,12 +875,14 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
       tab[x] = SENT;
       masks[x] = 0u;
     }
+    lposs[x] = 0u;
   }
   for (int x = t; x < kFilterWordsQ; x += kTableThreads) bits[x] = 0u;
   if (t == 0) {
     n_codes = 0;
     zero_at = -1;
     sent_mask = 0u;
+    sent_pos = 0u;
     int32_t run = 0;
     for (int c = 0; c < w.nch; ++c) {
       start[c] = run;
@@ -875,6 +897,7 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   for (int f0 = t; f0 < total; f0 += U * kTableThreads) {
     CodeT code[U];
     int chunk[U];
+    uint32_t pos[U];  // the code's latest key in that chunk, as a sub-call position
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int f = f0 + u * kTableThreads;
@@ -884,8 +907,9 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
         if (start[mid] <= f) lo = mid; else hi = mid;
       }
       chunk[u] = f < total ? lo : -1;
-      code[u] = f < total ? qlist[((p * w.nch + lo) * kParts + qt) * kChunk + (f - start[lo])]
-                          : CodeT(0);
+      const int64_t li = ((p * w.nch + lo) * kParts + qt) * kChunk + (f - start[lo]);
+      code[u] = f < total ? qlist[li] : CodeT(0);
+      pos[u] = f < total ? w.qlpos[li] : 0u;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -906,11 +930,13 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
             const unsigned long long k = atomicCAS(&tab[s], 0ull, bit | code[u]);
             if (k == 0) {  // entered
               entered = true;
+              atomicMax(&lposs[s], pos[u]);
               if (code[u] == 0) zero_at = s;
               break;
             }
             if (gt_code(k) == code[u]) {
               atomicOr(&tab[s], bit);
+              atomicMax(&lposs[s], pos[u]);
               break;
             }
             s = (s + 1) & (sub - 1);
@@ -919,6 +945,7 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
           const uint32_t bit = 1u << chunk[u];
           if (code[u] == SENT) {
             atomicOr(&sent_mask, bit);  // kept apart, takes no entry
+            atomicMax(&sent_pos, pos[u]);
           } else {
             for (int left = sub; left > 0; --left) {
               const unsigned long long k =
@@ -926,6 +953,7 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
                             static_cast<unsigned long long>(code[u]));
               if (k == SENT || k == code[u]) {  // entered, or the code's entry
                 atomicOr(&masks[s], bit);
+                atomicMax(&lposs[s], pos[u]);
                 entered = k == SENT;
                 if (entered && code[u] == 0) zero_at = s;
                 break;
@@ -946,7 +974,10 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   const int64_t base = (p << w.cap_log2) + static_cast<int64_t>(qt) * sub;
   if (t == 0) {
     w.spilled[blockIdx.x] = spill ? 1 : 0;
-    if constexpr (!k32) w.smask[blockIdx.x] = sent_mask;
+    if constexpr (!k32) {
+      w.smask[blockIdx.x] = sent_mask;
+      w.spos[blockIdx.x] = sent_pos;
+    }
     if (gt_part<CodeT>(splitmix_fin(CodeT(0))) == qt)
       w.zero_slot[p] = !spill && zero_at >= 0 ? base + zero_at : -1;
   }
@@ -956,6 +987,7 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
   for (int x = t; x < sub; x += kTableThreads) {
     w.gt[base + x] = tab[x];
     if constexpr (!k32) w.gmask[base + x] = masks[x];
+    w.gpos[base + x] = lposs[x];
   }
 }
 
@@ -1039,29 +1071,27 @@ __device__ __forceinline__ int bulk_insert_key(const StoreArgs& a, int64_t p, ui
   return r;
 }
 
-// A code of the group table with its chunk mask: its latest key is in the highest chunk of
-// the mask. Names the copy as bulk_place_key does (`row` null: nothing to copy).
-template <typename CodeT>
-__device__ __forceinline__ int bulk_place_masked(const StoreArgs& a, const BulkWs& w, int64_t p,
-                                                 CodeT code, uint32_t mask, uint8_t*& row,
+// A code of the group table with its chunk mask and its latest key `pos` (a sub-call
+// position, kept by the table kernel), which lies in the highest chunk of the mask. Names the
+// copy as bulk_place_key does (`row` null: nothing to copy).
+__device__ __forceinline__ int bulk_place_latest(const StoreArgs& a, int64_t p, uint64_t code,
+                                                 uint32_t mask, uint32_t pos, uint8_t*& row,
                                                  const uint8_t*& from) {
-  const int c2 = 31 - __clz(mask);
-  const int32_t lp = chunk_find<CodeT>(w, p, c2, code);
-  if (lp < 0) {  // the summary of a chunk in the mask holds the code; fail loudly
+  const int c2 = static_cast<int>(pos / kChunk);
+  if (mask == 0 || c2 != 31 - __clz(mask)) {  // the two always agree; fail loudly if not
     atomicOr(a.full, 2);
     row = nullptr;
     return 0;
   }
-  return bulk_place_key(a, p, code, c2, lp, row, from);
+  return bulk_place_key(a, p, code, c2, static_cast<int32_t>(pos % kChunk), row, from);
 }
 
-// bulk_place_masked with the lane's own copy.
-template <typename CodeT>
-__device__ __forceinline__ int bulk_insert_masked(const StoreArgs& a, const BulkWs& w, int64_t p,
-                                                  CodeT code, uint32_t mask) {
+// bulk_place_latest with the lane's own copy.
+__device__ __forceinline__ int bulk_insert_latest(const StoreArgs& a, int64_t p, uint64_t code,
+                                                  uint32_t mask, uint32_t pos) {
   uint8_t* row;
   const uint8_t* from = nullptr;
-  const int r = bulk_place_masked<CodeT>(a, w, p, code, mask, row, from);
+  const int r = bulk_place_latest(a, p, code, mask, pos, row, from);
   if (row) group_copy<1>(a, row, from, 0);
   return r;
 }
@@ -1092,15 +1122,15 @@ __global__ __launch_bounds__(256) void bulk_insert_kernel(StoreArgs a, BulkWs w)
     if constexpr (sizeof(CodeT) == 4) {
       const unsigned long long word = w.gt[g];
       if (word != 0 && gt_code(word) != 0)
-        claimed = bulk_place_masked<CodeT>(a, w, p, gt_code(word), static_cast<uint32_t>(word >> 32),
-                                           row, from);
+        claimed = bulk_place_latest(a, p, gt_code(word), static_cast<uint32_t>(word >> 32),
+                                    w.gpos[g], row, from);
     } else {
       const CodeT code = w.gt[g];
       if (code != SENT && code != 0)
-        claimed = bulk_place_masked<CodeT>(a, w, p, code, w.gmask[g], row, from);
+        claimed = bulk_place_latest(a, p, code, w.gmask[g], w.gpos[g], row, from);
       if (in_q == 0 && gt_part<CodeT>(splitmix_fin(SENT)) == qt) {
         const uint32_t m = w.smask[p * kParts + qt];
-        if (m) claimed += bulk_insert_masked<CodeT>(a, w, p, SENT, m);
+        if (m) claimed += bulk_insert_latest(a, p, SENT, m, w.spos[p * kParts + qt]);
       }
     }
     wave_copy_rows(a, row, from);
@@ -1144,7 +1174,7 @@ __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, i
       const int64_t g = w.zero_slot[p];
       if (g >= 0) {
         const uint32_t m = sizeof(CodeT) == 4 ? static_cast<uint32_t>(w.gt[g] >> 32) : w.gmask[g];
-        r = bulk_insert_masked<CodeT>(a, w, p, CodeT(0), m);
+        r = bulk_insert_latest(a, p, 0ull, m, w.gpos[g]);
       }
     } else {  // spilled part: code 0's latest chunk from the summaries
       for (int c = w.nch - 1; c >= 0; --c) {
@@ -1167,7 +1197,8 @@ __global__ __launch_bounds__(256) void bulk_zero_kernel(StoreArgs a, BulkWs w, i
 // Workspace layout of a bulk call of P partitions (sub-calls of S positions).
 struct BulkLayout {
   int64_t cap, cap_log2, nch, off_gmask, off_smask, off_spill, off_zero, off_scode, off_spos,
-      off_src, off_qlist, off_qcount, off_claims, off_filter, bytes;
+      off_src, off_qlist, off_qlpos, off_qcount, off_gpos, off_sposq, off_claims, off_filter,
+      bytes;
 };
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -1177,7 +1208,7 @@ BulkLayout bulk_layout(int64_t P, int64_t T, int32_t code_bytes) {
   const int64_t parts = code_bytes == 4 ? GtTraits<uint32_t>::kParts : GtTraits<uint64_t>::kParts;
   const int64_t S = T < kBulkSpan ? T : kBulkSpan;
   L.cap = 256 * parts;
-  L.cap_log2 = code_bytes == 4 ? 10 : 11;
+  L.cap_log2 = 8 + (parts == 8 ? 3 : 2);
   while (L.cap < 2 * S) {
     L.cap <<= 1;
     ++L.cap_log2;
@@ -1200,8 +1231,14 @@ BulkLayout bulk_layout(int64_t P, int64_t T, int32_t code_bytes) {
   o += align256(P * S * 4);
   L.off_qlist = o;
   o += align256(P * L.nch * parts * kChunk * code_bytes);
+  L.off_qlpos = o;
+  o += align256(P * L.nch * parts * kChunk * 2);
   L.off_qcount = o;
   o += align256(P * L.nch * parts * 4);
+  L.off_gpos = o;
+  o += align256(P * L.cap * 4);
+  L.off_sposq = o;
+  o += align256(P * parts * 4);
   L.off_claims = o;
   o += align256(P * L.cap / 256 * 4);
   L.off_filter = o;
@@ -1254,7 +1291,10 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
   w.sum_pos = reinterpret_cast<int32_t*>(ws + L.off_spos);
   w.src_in = reinterpret_cast<int32_t*>(ws + L.off_src);
   w.qlist = ws + L.off_qlist;
+  w.qlpos = reinterpret_cast<uint16_t*>(ws + L.off_qlpos);
   w.qcount = reinterpret_cast<int32_t*>(ws + L.off_qcount);
+  w.gpos = reinterpret_cast<uint32_t*>(ws + L.off_gpos);
+  w.spos = reinterpret_cast<uint32_t*>(ws + L.off_sposq);
   w.claims = reinterpret_cast<uint32_t*>(ws + L.off_claims);
   w.filter = reinterpret_cast<uint32_t*>(ws + L.off_filter);
   w.cap = static_cast<int32_t>(L.cap);

@@ -295,7 +295,7 @@ def _splitmix_fin(x):
     return x ^ (x >> np.uint64(31))
 
 
-def _bulk_group_cap(T, parts=4):
+def _bulk_group_cap(T, parts=8):
     s = min(T, 32 * 1024)
     cap = 256 * parts
     while cap < 2 * s:
@@ -303,18 +303,18 @@ def _bulk_group_cap(T, parts=4):
     return cap
 
 
-def test_bulk_spilled_quarter(dev):
-    """Key codes chosen so that one quarter of a partition's group table gets more codes than
-    its LDS table takes (3/4 of its words): that quarter's queries and inserts search the chunk
-    summaries instead, code 0 among them. Another partition uses the same quarter with few
-    codes and a third ordinary codes; two calls, against the dict."""
+def test_bulk_spilled_part_32bit(dev):
+    """32-bit key codes chosen so that one of a partition's eight group-table parts gets more
+    codes than its LDS table takes (3/4 of its words): that part's queries and inserts search
+    the chunk summaries instead, code 0 among them. Another partition uses the same part with
+    few codes and a third ordinary codes; two calls, against the dict."""
     rng = np.random.default_rng(18)
     P, T = 3, 6000
     cand = rng.integers(1, 1 << 31, size=200_000, dtype=np.int64)
-    q0 = cand[(_splitmix_fin(cand) >> np.uint64(62)) == 0]           # codes of quarter 0
-    assert int(_splitmix_fin(0) >> np.uint64(62)) == 0               # code 0 is one of them
+    q0 = cand[(_splitmix_fin(cand) >> np.uint64(61)) == 0]           # codes of part 0
+    assert int(_splitmix_fin(0) >> np.uint64(61)) == 0               # code 0 is one of them
     pools = [np.concatenate([[0], q0[:5500]]), q0[5500:6000], cand[:3000]]
-    limit = _bulk_group_cap(T) // 4 // 4 * 3
+    limit = _bulk_group_cap(T) // 8 // 4 * 3
     store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=200_000, device=dev)
     ref = oracle.DictStore(P, 2 * D_V)
     for call in range(2):
@@ -509,7 +509,7 @@ def test_bulk_64bit_spilled_part(dev):
              np.concatenate([[-1], ps[:5000]]),    # fills the all-ones code's part
              pz[5000:5300],                        # the same part as the first, few codes
              cand[:3000]]                          # ordinary codes
-    limit = _bulk_group_cap(T, parts=8) // 8 // 4 * 3
+    limit = _bulk_group_cap(T) // 8 // 4 * 3
     store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=300_000, device=dev)
     ref = oracle.DictStore(P, 2 * D_V)
     for call in range(2):
