@@ -846,8 +846,8 @@ __device__ __forceinline__ bool summary_slot(const BulkWs& w, int64_t p, int c, 
 }
 
 // One workgroup per (partition, part): the part's table built in LDS from the part's code
-// lists of every chunk of the partition, one CAS (new code) or OR (its chunk bit) per code and
-// chunk, then written out whole. With more than 3/4 of the part's entries taken the part is
+// lists of every chunk of the partition, one CAS (new code) or OR (its chunk bit) and one max
+// (its latest key) per code and chunk, then written out whole. With more than 3/4 of the part's entries taken the part is
 // marked spilled and the table is not written (codes met after that are not entered; one that
 // finds no free entry can only do so with the table past that mark).
 template <typename CodeT>
