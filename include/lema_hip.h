@@ -115,8 +115,7 @@ int lema_store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc
 
 /* Workspace bytes lema_store_exchange_ws needs for a call of n items, T positions per
  * partition and code_bytes codes; 0 when such a call does not use one: T <= 1024, or
- * T <= 2048 with more than 128 partitions, or T <= 4096 with 512 or more (the chunked path is
- * the faster one there). No reference counterpart: lema_store_exchange's long calls made
+ * T <= 2048 with more than 128 partitions (the chunked path is the faster one there). No reference counterpart: lema_store_exchange's long calls made
  * parallel. */
 int64_t lema_store_workspace_bytes(int64_t n, int64_t T, int32_t code_bytes);
 

@@ -89,8 +89,8 @@ class HashStore:
         out rows of `vbytes` bytes in any dtype. `qcodes=None` only inserts. With `check` the
         full flag is read back (a device sync) and a full table raises like the reference;
         without it, call `check_full()` later (e.g. after a graph replay). A long call
-        (T > 1024 with at most 128 partitions, T > 2048 with fewer than 512, T > 4096 beyond)
-        takes the bulk path with a device workspace this store keeps."""
+        (T > 1024 with at most 128 partitions, T > 2048 with more) takes the bulk path with
+        a device workspace this store keeps."""
         kc, cb = _codes(kcodes)
         n = kc.numel()
         if qcodes is not None:

@@ -1260,16 +1260,18 @@ namespace {
 // Bulk or chunked, by partitions P and positions T per call. A chunked launch runs one
 // workgroup per partition, so with few partitions most of the chip idles through the T/1024
 // launches in order, while the bulk kernels' costs per sub-call and per partition only pay
-// off over long enough calls. Measured on one MI355X (64-bit codes, 48- and 128-byte value
-// rows, microseconds chunked / bulk): T = 1024 is a tie or a loss for bulk at any P (24: 42 /
-// 49; 1024: 166 / 322); T = 2048 wins from 24 to 128 partitions (24: 85 / 56; 128: 109 / 100)
-// and loses from 256 (256: 115 / 147); T = 4096 wins up to 256 partitions (256: 272 / 252)
-// and loses at 1024 (740 / 872); T = 16384 wins everywhere (1024: 3169 / 3011).
+// off over long enough calls. Measured on one MI355X with 64-bit codes and 48- and 128-byte
+// value rows, microseconds chunked / bulk, on a fresh table (every key claims a slot, as in a
+// prefill) and on one already holding the keys (overwrites only):
+//   T = 1024: claims 107 / 91 at 128 partitions, 274 / 383 at 1024; overwrites 42 / 49 at 24;
+//   T = 2048: claims 205 / 116 at 128, 205 / 164 at 256, 241 / 335 and 427 / 401 at 512;
+//             overwrites 85 / 56 at 24, 115 / 147 at 256;
+//   T = 4096: claims 597 / 558 and 846 / 659 at 512, 1236 / 1032 and 1859 / 1300 at 1024;
+//             overwrites 740 / 872 at 1024;
+//   T = 16384: bulk ahead everywhere (overwrites at 1024 partitions: 3169 / 3011).
 bool bulk_applies(int64_t P, int64_t T) {
   if (T <= 1024) return false;
-  if (P <= 128) return true;
-  if (P >= 512) return T > 4096;
-  return T > 2048;
+  return P <= 128 || T > 2048;
 }
 
 template <typename CodeT>

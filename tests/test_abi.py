@@ -62,12 +62,11 @@ def test_host_validation_statuses(L):
 
 @pytest.mark.parametrize("P,T,bulk", [
     (24, 1024, False), (24, 1025, True), (128, 2048, True), (129, 2048, False),
-    (129, 2049, True), (511, 2049, True), (512, 4096, False), (512, 4097, True),
-    (4096, 16384, True), (1, 1, False)])
+    (129, 2049, True), (4096, 2048, False), (4096, 2049, True), (4096, 16384, True),
+    (1, 1, False)])
 def test_store_workspace_only_where_bulk_is_faster(L, P, T, bulk):
     """A store workspace (the bulk path) is asked for exactly where the bulk path was the
-    faster one in measurement: T > 1024 up to 128 partitions, T > 2048 below 512, T > 4096
-    from 512 on."""
+    faster one in measurement: T > 1024 up to 128 partitions, T > 2048 beyond."""
     for cb in (4, 8):
         assert (L.lema_store_workspace_bytes(P * T, T, cb) > 0) == bulk, (P, T, cb)
     assert L.lema_store_workspace_bytes(P * T, T, 2) == 0

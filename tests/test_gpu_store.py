@@ -81,10 +81,10 @@ def test_store_one_shot(dev):
 
 
 def test_store_long_call_spans_subchunks(dev):
-    """T = 2500 per call over 600 partitions: the chunked path, three 1024-position sub-chunks
-    in order within one exchange."""
-    assert _lib.lib().lema_store_workspace_bytes(600 * 2500, 2500, 4) == 0
-    run_dict_case(dev, seed=5, P=600, T=2500, chunk=2500, n_codes=60, capacity=120_000,
+    """T = 2040 per call over 600 partitions: the chunked path, two sub-chunks (1024 and 1016
+    positions) in order within one exchange."""
+    assert _lib.lib().lema_store_workspace_bytes(600 * 2040, 2040, 4) == 0
+    run_dict_case(dev, seed=5, P=600, T=2040, chunk=2040, n_codes=60, capacity=120_000,
                   code_dtype=torch.int32)
 
 
