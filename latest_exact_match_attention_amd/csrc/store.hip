@@ -883,12 +883,16 @@ __global__ __launch_bounds__(kTableThreads) void bulk_table_kernel(BulkWs w) {
     zero_at = -1;
     sent_mask = 0u;
     sent_pos = 0u;
-    int32_t run = 0;
-    for (int c = 0; c < w.nch; ++c) {
-      start[c] = run;
-      run += w.qcount[(p * w.nch + c) * kParts + qt];
+  }
+  if (t < 64) {  // the part's codes before each chunk: one load per lane, scanned in the wave
+    const int32_t cnt = t < w.nch ? w.qcount[(p * w.nch + t) * kParts + qt] : 0;
+    int32_t incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t y = __shfl_up(incl, o);
+      if (t >= o) incl += y;
     }
-    start[w.nch] = run;
+    if (t <= w.nch) start[t] = incl - cnt;  // t == nch: the part's total
   }
   __syncthreads();
   const int total = start[w.nch];
