@@ -98,6 +98,17 @@ def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def widen_codes(t: torch.Tensor) -> torch.Tensor:
+    """Codes in the int64 carrier, for calls that mix widths. An int32 code stands for its
+    32-bit pattern, which the kernels read as an unsigned word (a d_qk <= 32 code of the
+    reference is an int64 below 2^32), so it is zero-extended, never sign-extended."""
+    if t.dtype == torch.int64:
+        return t
+    if t.dtype == torch.int32:
+        return t.to(torch.int64) & 0xFFFFFFFF
+    return t.to(torch.int64)
+
+
 def require_device(*ts: torch.Tensor) -> None:
     for t in ts:
         if not t.is_cuda:

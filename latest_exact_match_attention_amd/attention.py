@@ -67,7 +67,7 @@ def _codes_pair(qc: torch.Tensor, kc: torch.Tensor) -> tuple[torch.Tensor, torch
         raise ValueError(f"query and key codes differ in shape: {tuple(qc.shape)} vs "
                          f"{tuple(kc.shape)}")
     if qc.dtype != kc.dtype:
-        qc, kc = qc.to(torch.int64), kc.to(torch.int64)
+        qc, kc = _lib.widen_codes(qc), _lib.widen_codes(kc)
     if qc.dtype not in (torch.int64, torch.int32, torch.uint32, torch.uint64):
         raise TypeError(f"codes must be int64 or int32, got {qc.dtype}")
     return qc.contiguous(), kc.contiguous(), qc.element_size()

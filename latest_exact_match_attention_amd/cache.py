@@ -96,7 +96,7 @@ class HashStore:
         if qcodes is not None:
             qc, qcb = _codes(qcodes)
             if qcb != cb:
-                qc, kc, cb = qc.to(torch.int64), kc.to(torch.int64), 8
+                qc, kc, cb = _lib.widen_codes(qc), _lib.widen_codes(kc), 8
             if qc.numel() != n:
                 raise ValueError("query and key codes differ in count")
         else:

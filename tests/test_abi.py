@@ -89,3 +89,13 @@ def test_python_api_refuses_cpu_tensors():
         lema_hard(q, q, q)
     with pytest.raises(ValueError, match="> 64"):
         pack_codes(torch.randn(2, 65))
+
+
+def test_widen_codes_zero_extends_int32():
+    """Mixed-width calls widen int32 codes to the int64 code with the same 32-bit pattern,
+    which is what the kernels read (an unsigned word), never the sign-extended value."""
+    t = torch.tensor([-7, -1, 0, 5, -(1 << 31)], dtype=torch.int32)
+    got = _lib.widen_codes(t).tolist()
+    assert got == [(1 << 32) - 7, (1 << 32) - 1, 0, 5, 1 << 31]
+    w = torch.tensor([-7, 1 << 40], dtype=torch.int64)
+    assert _lib.widen_codes(w) is w

@@ -164,3 +164,42 @@ def test_full_lm_forward_loss_matches_oracle(dev):
         assert abs(ours - want) <= 1e-2 * abs(want), (ours, want)
         check_layers(m, cfg, x, m.state_dict())
     print(f"full LM loss {ours:.6f} (oracle {want:.6f})", flush=True)
+
+
+@pytest.mark.parametrize("name", ["d16", "d40"])
+def test_model_matches_reference_fixture(dev, name):
+    """The product model in fp32 on the GPU against the reference's own model
+    (tests/golden/model.npz, written from code/lema/model.py): parameters drawn on the CPU
+    with the fixture's seed, k_proj tied to q_proj as in the fixture, then every layer's
+    codes and match indices from the HIP path equal the reference's, and the loss is within
+    1e-5 relative of the reference's."""
+    from pathlib import Path
+
+    import numpy as np
+
+    from latest_exact_match_attention_amd.analysis import trace
+    g = np.load(Path(__file__).resolve().parent / "golden" / "model.npz")
+    vocab, depth, dim, heads, d_qk, d_v, dim_ff, seed = g[f"{name}/config"].tolist()
+    cfg = ModelConfig(vocab_size=vocab, depth=depth, dim=dim, num_heads=heads, d_qk=d_qk,
+                      d_v=d_v, dim_ff=dim_ff)
+    torch.manual_seed(seed)
+    m = Transformer(cfg)
+    with torch.no_grad():
+        for blk in m.blocks:
+            blk.attn.k_proj.weight.copy_(blk.attn.q_proj.weight)
+    m = m.to(dev).eval().requires_grad_(False)
+    m.set_hard(True)
+    tok = torch.from_numpy(g[f"{name}/tokens"]).to(dev)
+    x, y = tok[:, :-1], tok[:, 1:]
+    logits, recs = trace(m, x)
+    for i, rec in enumerate(recs):
+        for key in ("qc", "kc", "src"):
+            assert np.array_equal(rec[key].cpu().numpy(), g[f"{name}/{key}"][i]), (i, key)
+    with torch.no_grad():
+        loss = torch.nn.functional.cross_entropy(logits.float().reshape(-1, logits.shape[-1]),
+                                                 y.reshape(-1)).item()
+        ours = lm_loss(m, x, y, chunk=16).item()
+    ref = float(g[f"{name}/loss"])
+    assert abs(loss - ref) <= 1e-5 * abs(ref), (loss, ref)
+    assert abs(ours - ref) <= 1e-5 * abs(ref), (ours, ref)
+    assert np.abs(logits.float().cpu().numpy() - g[f"{name}/logits"]).max() <= 1e-3

@@ -140,6 +140,27 @@ def test_latest_match_all_ones_code(dev, code_dtype):
     assert (got[1, 1501:] == 1500).all() and (got[1, :1501] == -1).all()
 
 
+def test_latest_match_mixed_widths_zero_extend(dev):
+    """An int32 code is its 32-bit pattern: mixed with int64 codes it must match the int64
+    code below 2^32 with the same bits, also when bit 31 is set (half of all 32-bit codes),
+    never the sign-extended negative int64."""
+    rng = np.random.default_rng(31)
+    T = 3000
+    pats = (np.arange(40, dtype=np.int64) * 0x9E3779B1) & 0xFFFFFFFF
+    assert (pats >= 1 << 31).any() and (pats < 1 << 31).any()
+    qc = rng.choice(pats, size=(3, T))
+    kc = rng.choice(pats, size=(3, T))
+    kc[2, ::5] -= 1 << 32          # sign-extended twins: these keys must NOT match
+    want = oracle.latest_prev_match(qc, kc)
+    q32 = torch.from_numpy(qc.astype(np.uint32).view(np.int32)).to(dev)
+    k64 = torch.from_numpy(kc).to(dev)
+    got = latest_prev_match(q32, k64).cpu().numpy()
+    assert np.array_equal(got, want)
+    assert (got >= 0).mean() > 0.5
+    got = latest_prev_match(torch.from_numpy(kc).to(dev), q32).cpu().numpy()
+    assert np.array_equal(got, oracle.latest_prev_match(kc, qc))
+
+
 def test_latest_match_structured_rows(dev):
     T = 4100
     i = np.arange(T)

@@ -122,6 +122,37 @@ def test_store_contended_decode(dev):
     assert grp.numel() == len(store)                   # every claimed slot published once
 
 
+@pytest.mark.parametrize("T", [1, 700, 3000])
+def test_store_mixed_widths_zero_extend(dev, T):
+    """Keys inserted as int64 codes below 2^32 are found by int32 queries of the same 32-bit
+    pattern (bit 31 set in half of them) and the other way round; the table holds the
+    zero-extended code, as the reference's int64 code (decode-sized, chunked and bulk
+    calls)."""
+    rng = np.random.default_rng(T)
+    P = 16
+    pats = (np.arange(1, 200, dtype=np.int64) * 0x9E3779B1) & 0xFFFFFFFF
+    assert (pats >= 1 << 31).sum() > 50
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=40_000, device=dev)
+    ref = oracle.DictStore(P, 2 * D_V)
+    for step in range(3):
+        qc = rng.choice(pats, size=P * T)
+        kc = rng.choice(pats, size=P * T)
+        v = rng.integers(0, 1 << 16, size=(P * T, D_V), dtype=np.uint16)
+        q32 = torch.from_numpy(qc.astype(np.uint32).view(np.int32)).to(dev)
+        k64 = torch.from_numpy(kc).to(dev)
+        if step == 1:              # the other pairing: int64 queries, int32 keys
+            q32 = torch.from_numpy(qc).to(dev)
+            k64 = torch.from_numpy(kc.astype(np.uint32).view(np.int32)).to(dev)
+        out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+        store.exchange(q32, k64, torch.from_numpy(v.view(np.int16)).to(dev), out, T, 0)
+        want = ref.exchange(qc, kc, v.view(np.uint8).reshape(-1, 2 * D_V), T, 0)
+        assert np.array_equal(out.cpu().numpy().view(np.uint8).reshape(-1, 2 * D_V), want), step
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    grp, code, _ = store.dump()
+    got = set(zip(grp.cpu().numpy().tolist(), code.cpu().numpy().tolist()))
+    assert got == {(p, k) for p, d in enumerate(ref.ref) for k in d}
+
+
 def test_store_table_is_reference_format(dev):
     """A table filled on the GPU is continued by the C restatement of store.cpp on the host
     (same slot format and home-slot hash): the results stay those of the dict."""

@@ -160,3 +160,48 @@ def test_fused_decode_segments_decline_what_they_cannot_take():
     tok = torch.zeros(2, 1, dtype=torch.long)
     argmax_into(logits, tok)
     assert tok.view(-1).tolist() == [1, 0]
+
+
+class _HostStoreView:
+    """A stand-in for a layer's store view on the CPU: the exchange returns zeros like v (the
+    op trace, not the values, is what the test looks at)."""
+
+    def exchange(self, qc, kc, v, check=True):
+        return torch.zeros(v.shape, dtype=v.dtype)
+
+
+class _HostCache:
+    def __init__(self, depth):
+        self.t, self._v = 0, [_HostStoreView() for _ in range(depth)]
+
+    def layer(self, i):
+        return self._v[i]
+
+
+def test_forward_and_decode_step_issue_no_batched_products(monkeypatch):
+    """Transformer.forward (dense and through a cache) and one decode step's work -- the
+    cached forward of one token per stream, then the greedy pick -- in bf16 on the CPU with
+    the device-only exact op stubbed by the oracle's: no aten::bmm anywhere (every product is
+    a plain 2-D GEMM), the form a bf16 batched product with a transposed operand takes."""
+    from latest_exact_match_attention_amd import model as M
+    monkeypatch.setattr(M, "lema_hard", lambda q, k, v: torch_model.lema_exact(q, k, v)[0])
+    monkeypatch.setattr(M, "pack_codes", lambda z, dt=torch.int64: torch_model.pack(z).to(dt))
+    cfg = ModelConfig(vocab_size=256, depth=2, dim=64, num_heads=4, d_qk=16, d_v=16)
+    torch.manual_seed(0)
+    m = Transformer(cfg).to(torch.bfloat16).eval().requires_grad_(False)
+    m.set_hard(True)
+    x = torch.randint(0, 256, (2, 48))
+    with torch.no_grad():
+        ops = _aten_ops(lambda: m(x))
+        assert "aten::mm" in ops and "aten::bmm" not in ops, sorted(ops)
+        cache = _HostCache(cfg.depth)
+        ops = _aten_ops(lambda: m(x, cache=cache))
+        assert "aten::bmm" not in ops, sorted(ops)
+        tok = torch.zeros(2, 1, dtype=torch.long)
+
+        def step():
+            logits = m(tok, cache=cache)
+            M.argmax_into(logits, tok)
+        ops = _aten_ops(step)
+        assert "aten::bmm" not in ops, sorted(ops)
+        assert cache.t == 48 + 1
