@@ -1,8 +1,14 @@
 """Benchmark of the LEMA hot path on one MI355X; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload zipf_prefill|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|zipf_prefill|decode|...]
 
-zipf_prefill (default): B8 H16 T16384, 24-bit Zipf(1.1) codes over 4096 distinct codes per
+all (default): the zipf_prefill line below, with the decode, long_context and lm_forward
+workloads run after it in the same process and carried as sub-records of the one JSON line
+("decode", "long_context", "lm_forward": each with its own value, unit, ms_per_step,
+roofline, cpu_baseline and parity flags). --steps and --warmup apply to the prefill line;
+the sub-records use their own workload's defaults (lm_forward: 3 steps after 1 warm-up).
+
+zipf_prefill: B8 H16 T16384, 24-bit Zipf(1.1) codes over 4096 distinct codes per
 (b, h), d_v 64 bf16. A step is one fused resolve+gather launch over the whole batch, inputs
 resident in HBM: per query it reads the query and key code (4 + 4 B) and a value row
 (128 B, compulsory once) and writes the match index (4 B) and the output row (128 B):
@@ -88,8 +94,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="zipf_prefill",
-                    choices=["zipf_prefill", "decode", "lm_forward", "long_context",
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "zipf_prefill", "decode", "lm_forward", "long_context",
                              "decode_model"])
     ap.add_argument("--dm-batch", type=int, default=16)
     ap.add_argument("--dm-prompt", type=int, default=4096)
@@ -115,6 +121,17 @@ def parse():
                     help="also run one plain device copy of the value tensor (known bytes), "
                          "to calibrate profiler memory counters")
     return ap.parse_args()
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def load_traffic(name: str):
@@ -150,6 +167,7 @@ def cpu_baseline_prefill(qc, kc, v32, rows: int):
     times.sort()
     med = times[len(times) // 2]
     return {"value": rows * T / med, "unit": "queries/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{rows} of {B * H} (b,h) rows x T={T} ({rows * T} queries), bf16 "
                       f"d_v {v.shape[-1]}; median of {len(times)} runs, "
                       f"{med * 1e3:.1f} ms per run"}
@@ -344,7 +362,7 @@ def bench_decode(a):
         hits = float((got.view(steps, P, dv) != 0).any(-1).float().mean())
         med = sorted(times)[len(times) // 2]
         cpu = {"value": 1.0 / med, "unit": "decode steps/s", "cores": threads,
-               "kind": "reference",
+               "kind": "reference", "cpu_model": cpu_model(),
                "sample": f"all {steps} steps of the workload through code/lema/csrc/store.cpp "
                          f"(compiled from source, OpenMP, grain 128/T) on a host table in "
                          f"the same state; median {med * 1e6:.1f} us/step, mean "
@@ -413,6 +431,7 @@ def cpu_baseline_lm(model, cfg, tokens: int):
             times.append(time.perf_counter() - t0)
     med = sorted(times)[len(times) // 2]
     return {"value": tokens / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"batch 1 x {tokens} tokens of the same model (fp32 weights), forward + "
                       f"loss; median of {len(times)} runs, {med:.2f} s per run; per-token "
                       f"cost grows with T only through the exact op's sort"}
@@ -552,7 +571,7 @@ def bench_long(a):
         torch.empty_like(probe).copy_(probe)
         torch.cuda.synchronize()
         del probe
-    total_ms, per_call, cpu_s, same = 0.0, [], [], True
+    total_ms, per_call, cpu_s, same, counts_same = 0.0, [], [], True, True
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for c in range(calls):
         qc64, kc64 = long_context_codes(0, H, c * L, (c + 1) * L, dev)
@@ -578,8 +597,9 @@ def bench_long(a):
             host_counts += ref.exchange(host_table, qh, kh, vh, oh, L, 0, cap_h, 2 * dv)
             cpu_s.append(time.perf_counter() - t0)
             same = same and bool(torch.equal(out.view(torch.int16).cpu(), oh))
-            print(f"  reference store: {cpu_s[-1]:.2f} s, outputs identical: {same}",
-                  file=sys.stderr, flush=True)
+            counts_same = counts_same and bool(torch.equal(store.counts, host_counts))
+            print(f"  reference store: {cpu_s[-1]:.2f} s, outputs identical: {same}, "
+                  f"counts identical: {counts_same}", file=sys.stderr, flush=True)
         del qc64, kc64, qc, kc, v, out
     nq = H * L * calls
     bpq = 4 + 4 + 4 + 2 * 2 * dv
@@ -587,15 +607,14 @@ def bench_long(a):
     cpu = None
     parity = None
     if n_par:
-        counts_same = bool(torch.equal(store.counts, host_counts)) if n_par == calls else None
         parity = {"calls_checked": n_par, "outputs_identical": same,
-                  "counts_identical": counts_same}
+                  "counts_identical_after_checked_calls": counts_same}
         cpu = {"value": H * L * n_par / sum(cpu_s), "unit": "queries/s", "cores": threads,
-               "kind": "reference",
+               "kind": "reference", "cpu_model": cpu_model(),
                "sample": f"the first {n_par} call(s) of 64 x 2^20 positions through "
                          f"code/lema/csrc/store.cpp (compiled from source, OpenMP) on a host "
                          f"table of {cap_h} slots; {sum(cpu_s):.2f} s"}
-        if not same:
+        if not (same and counts_same):
             print("long_context parity FAILED", file=sys.stderr)
     return {
         "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
@@ -716,11 +735,33 @@ def main():
         print(f"bench.py measures one GPU only (there is no multi-GPU path); got "
               f"--gpus {a.gpus}", file=sys.stderr)
         return 2
-    run = {"decode": bench_decode, "lm_forward": bench_lm, "long_context": bench_long,
-           "decode_model": bench_decode_model}.get(a.workload, bench_prefill)
-    out = run(a)
+    runs = {"decode": bench_decode, "lm_forward": bench_lm, "long_context": bench_long,
+            "decode_model": bench_decode_model, "zipf_prefill": bench_prefill}
+    if a.workload != "all":
+        print(json.dumps(runs[a.workload](a)), flush=True)
+        return 0
+    out = bench_prefill(a)
+    print(f"zipf_prefill: {out['ms_per_step'] * 1e3:.1f} us/step, "
+          f"{out['roofline']['frac']:.3f} of HBM peak", file=sys.stderr, flush=True)
+    for name, steps, warmup in SUB_WORKLOADS:
+        import torch
+        torch.cuda.empty_cache()
+        sub = argparse.Namespace(**vars(a))
+        sub.workload = name
+        if steps is not None:
+            sub.steps, sub.warmup = steps, warmup
+        rec = runs[name](sub)
+        out[name] = {k: v for k, v in rec.items() if k not in SUB_DROP}
+        print(f"{name}: {rec['value']:.4g} {rec['unit']}, {rec['ms_per_step']:.4g} ms/step",
+              file=sys.stderr, flush=True)
     print(json.dumps(out), flush=True)
     return 0
+
+
+# the workloads carried as sub-records of the default line: (name, steps, warm-up) with None
+# keeping the workload's own step counts
+SUB_WORKLOADS = (("decode", None, None), ("long_context", None, None), ("lm_forward", 3, 1))
+SUB_DROP = ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline")
 
 
 if __name__ == "__main__":
