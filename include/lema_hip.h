@@ -130,6 +130,25 @@ int lema_store_exchange_ws(void* table, int64_t cap, int64_t vbytes, const void*
                            int64_t n, int64_t T, int64_t g0, int64_t* counts, int32_t* full,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of the device scratch array behind lema_store_exchange_noalloc, per GPU. */
+#define LEMA_NOALLOC_SCRATCH_BYTES (64LL * 1024 * 1024)
+
+/* lema_store_exchange with no workspace argument that allocates nothing: a call that takes
+ * the bulk path (as lema_store_workspace_bytes would report) runs on a scratch array inside
+ * the library, LEMA_NOALLOC_SCRATCH_BYTES per GPU, held from the first such call on that GPU
+ * until the process ends, in consecutive slices of its partitions sized to fit it. Same
+ * results as lema_store_exchange_ws. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops). Make the first
+ * call on a device outside graph capture (it looks the scratch's address up). Calls that
+ * overlap on one GPU (two streams, two threads) race on the shared scratch; calls in one
+ * stream's order do not. A call whose single partition needs more scratch than that is
+ * rejected with LEMA_BAD_ARG (none can at present: a sub-call spans at most 32,768
+ * positions, about 4.5 MB of scratch per partition). */
+int lema_store_exchange_noalloc(void* table, int64_t cap, int64_t vbytes, const void* qc,
+                                const void* kc, int32_t code_bytes, const void* values,
+                                void* out, int64_t n, int64_t T, int64_t g0, int64_t* counts,
+                                int32_t* full, void* stream);
+
 /* ---- fused model segments (bf16), what the reference compiles with torch.compile ---- */
 
 /* out = silu(gate) * up over n bf16 elements (n % 8 == 0, 16-byte aligned), the silu rounded

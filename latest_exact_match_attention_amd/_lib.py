@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "liblema_hip.so"
 OK, TABLE_FULL, BAD_ARG, HIP_ERROR = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
 MISS_DENSE, MISS_ZERO = 0, 1
+NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024   # LEMA_NOALLOC_SCRATCH_BYTES of the header
 
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -58,6 +59,8 @@ PROTOTYPES = {
     "lema_skinny_swiglu_bf16": ([_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _p], ctypes.c_int),
     "lema_skinny_norm_swiglu_bf16": ([_p, _p, _p, ctypes.c_float, _p, _p, _p, _i64, _i64, _i64,
                                       _i64, _p, _p], ctypes.c_int),
+    "lema_store_exchange_noalloc": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p,
+                                     _p, _p], ctypes.c_int),
     "lema_store_exchange_ws": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p, _p,
                                 _p, _i64, _p], ctypes.c_int),
 }

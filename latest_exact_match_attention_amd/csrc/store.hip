@@ -31,6 +31,8 @@
 //     the table; after a workgroup barrier (no query may see a later key) each key code's
 //     last occurrence overwrites its existing entry, and after another barrier the codes that
 //     had none claim new slots.
+#include <mutex>
+
 #include "resolve_core.h"
 
 namespace lema {
@@ -1423,4 +1425,96 @@ extern "C" int lema_store_exchange_ws(void* table, int64_t cap, int64_t vbytes, 
                                       void* stream) {
   return store_exchange(table, cap, vbytes, qc, kc, code_bytes, values, out, n, T, g0, counts,
                         full, workspace, workspace_bytes, stream);
+}
+
+// ---- the exchange without a workspace argument and without allocation ----
+//
+// The bulk path's workspace lives in `scratch`, one file-scope device array per GPU, held
+// until the process ends. Host code never passes `scratch` itself (in host code the name is a
+// host-side stand-in, not a device address): its address on a device is looked up once per
+// device with hipGetSymbolAddress, with that device current, and kept in scratch_ptr[].
+// Every call on a device shares its array and no call clears it (the bulk kernels rewrite
+// every word they read within a sub-call), so calls that overlap on one device -- on two
+// streams, or from two threads -- race; calls in one stream's order do not.
+constexpr int64_t kNoAllocScratchBytes = LEMA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+uint8_t* scratch_ptr[kMaxDevices];
+std::mutex scratch_mutex;
+
+// The device-side address of `scratch` on the device `stream` belongs to (the current device
+// for the null stream), looked up on the first call for that device.
+int scratch_address(hipStream_t st, uint8_t** out) {
+  int dev = 0;
+  if (st != nullptr) {
+    LEMA_HIP_CHECK(hipStreamGetDevice(st, &dev));
+  } else {
+    LEMA_HIP_CHECK(hipGetDevice(&dev));
+  }
+  LEMA_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d beyond the %d this library tracks",
+               dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_ptr[dev] == nullptr) {
+    int cur = 0;
+    LEMA_HIP_CHECK(hipGetDevice(&cur));
+    if (cur != dev) LEMA_HIP_CHECK(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) LEMA_HIP_CHECK(hipSetDevice(cur));
+    LEMA_HIP_CHECK(e);
+    LEMA_REQUIRE(p != nullptr && aligned(p, 256), "scratch of device %d is misaligned", dev);
+    scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = scratch_ptr[dev];
+  return LEMA_OK;
+}
+
+}  // namespace
+
+extern "C" int lema_store_exchange_noalloc(void* table, int64_t cap, int64_t vbytes,
+                                           const void* qc, const void* kc, int32_t code_bytes,
+                                           const void* values, void* out, int64_t n, int64_t T,
+                                           int64_t g0, int64_t* counts, int32_t* full,
+                                           void* stream) {
+  clear_error();
+  LEMA_REQUIRE(code_bytes == 4 || code_bytes == 8, "code_bytes must be 4 or 8, got %d", code_bytes);
+  LEMA_REQUIRE(T > 0 && n >= 0 && n % T == 0, "items must be partitions x T (n=%lld, T=%lld)",
+               (long long)n, (long long)T);
+  LEMA_REQUIRE(vbytes > 0 && vbytes % 8 == 0,
+               "value row of %lld bytes breaks slot alignment (must be a multiple of 8)",
+               (long long)vbytes);
+  const int64_t P = n / T;
+  if (n == 0 || !bulk_applies(P, T))      // decode steps and chunked calls use no scratch
+    return store_exchange(table, cap, vbytes, qc, kc, code_bytes, values, out, n, T, g0, counts,
+                          full, nullptr, 0, stream);
+  // Partitions never read one another's entries, so a call may run as consecutive slices of
+  // its partitions, each small enough for the scratch (bulk_applies holds for every slice:
+  // a slice is never longer and never has more partitions than the call).
+  const int64_t one = bulk_layout(1, T, code_bytes).bytes;
+  LEMA_REQUIRE(one <= kNoAllocScratchBytes,
+               "a partition of %lld positions needs %lld bytes of scratch, more than the %lld "
+               "this entry point has", (long long)T, (long long)one,
+               (long long)kNoAllocScratchBytes);
+  int64_t most = kNoAllocScratchBytes / one;
+  if (most > P) most = P;
+  while (bulk_layout(most, T, code_bytes).bytes > kNoAllocScratchBytes) --most;
+  const int64_t slices = (P + most - 1) / most;
+  const int64_t per = (P + slices - 1) / slices;
+  uint8_t* ws = nullptr;
+  if (int rc = scratch_address(static_cast<hipStream_t>(stream), &ws)) return rc;
+  for (int64_t p0 = 0; p0 < P; p0 += per) {
+    const int64_t ps = P - p0 < per ? P - p0 : per;
+    const int64_t i0 = p0 * T;
+    const void* q = qc != nullptr ? static_cast<const uint8_t*>(qc) + i0 * code_bytes : nullptr;
+    void* o = out != nullptr ? static_cast<uint8_t*>(out) + i0 * vbytes : nullptr;
+    if (int rc = store_exchange(table, cap, vbytes, q, static_cast<const uint8_t*>(kc) +
+                                    i0 * code_bytes, code_bytes,
+                                static_cast<const uint8_t*>(values) + i0 * vbytes, o, ps * T, T,
+                                g0 + p0, counts, full, ws, kNoAllocScratchBytes, stream))
+      return rc;
+  }
+  return LEMA_OK;
 }

@@ -99,3 +99,9 @@ def test_widen_codes_zero_extends_int32():
     assert got == [(1 << 32) - 7, (1 << 32) - 1, 0, 5, 1 << 31]
     w = torch.tensor([-7, 1 << 40], dtype=torch.int64)
     assert _lib.widen_codes(w) is w
+
+
+def test_noalloc_scratch_size_agrees_with_header():
+    text = (ROOT / "include" / "lema_hip.h").read_text()
+    m = re.search(r"#define LEMA_NOALLOC_SCRATCH_BYTES \((\d+)LL \* 1024 \* 1024\)", text)
+    assert m and int(m.group(1)) * 1024 * 1024 == _lib.NOALLOC_SCRATCH_BYTES
