@@ -114,6 +114,10 @@ def parse():
     ap.add_argument("--decode-prefill", type=int, default=262144,
                     help="keys prefilled per partition for the decode workload")
     ap.add_argument("--decode-steps", type=int, default=1024)
+    ap.add_argument("--step-stamps", action="store_true",
+                    help="decode: run the diagnostics build (build --stamps), whose step kernel "
+                         "reads the clock after each phase, and report the breakdown and the "
+                         "cost of an empty graph node")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16,
                     help="(b, h) rows of the workload timed for the CPU baseline")
@@ -278,7 +282,12 @@ def bench_decode(a):
     from latest_exact_match_attention_amd import build
     from latest_exact_match_attention_amd.cache import HashStore
 
-    if not build.LIB.exists():
+    from latest_exact_match_attention_amd import _lib
+    if a.step_stamps:
+        if not build.STAMPS_LIB.exists():
+            build.build(stamps=True)
+        L_st = _lib.use_stamps_library()
+    elif not build.LIB.exists():
         build.build()
     seqs, heads, dv = 16, 64, 24
     P, n0, steps = seqs * heads, a.decode_prefill, a.decode_steps
@@ -325,11 +334,17 @@ def bench_decode(a):
     kc = torch.randint(0, 2**32, (steps, P), dtype=torch.int64, device=dev, generator=gen)
     vv = torch.randn((steps, P, dv), device=dev, generator=gen).to(torch.bfloat16)
     out = torch.empty_like(vv)
+    stamps = None
+    if a.step_stamps:
+        stamps = torch.zeros((steps, P, 5), dtype=torch.int64, device=dev)
+        L_st.lema_debug_step_stamps(stamps.data_ptr())
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for s_ in range(steps):
             store.exchange(qc[s_], kc[s_], vv[s_], out[s_], 1, 0, check=False)
+    if a.step_stamps:
+        L_st.lema_debug_step_stamps(None)
     stream = torch.cuda.current_stream(dev)
     x = torch.empty(1 << 26, device=dev)
     for _ in range(20):                      # clocks up; the store is not touched
@@ -343,6 +358,7 @@ def bench_decode(a):
     store.check_full()
     ms_step = e0.elapsed_time(e1) / steps
     hits = None
+    breakdown = step_breakdown(stamps, L_st, P, steps, stream) if a.step_stamps else None
 
     cpu = None
     parity = None
@@ -399,7 +415,52 @@ def bench_decode(a):
                      "bytes_per_item": DECODE_BYTES_PER_ITEM, "items_per_launch": P},
         "cpu_baseline": cpu,
         "parity": parity,
+        **({"step_stamps": breakdown} if breakdown is not None else {}),
     }
+
+
+def step_breakdown(stamps, L, P: int, steps: int, stream) -> dict:
+    """Phases of the decode steps from the diagnostics build's clock readings (100 MHz, per
+    item: start, codes loaded, first windows read, claim done, value and count written), and
+    the per-step cost of a graph of empty kernels with the same grid."""
+    import numpy as np
+    import torch
+    d = stamps.cpu().numpy()
+    t = [d[..., k].astype(np.int64) for k in range(5)]
+    start, end = t[0].min(1), t[4].max(1)
+    us = lambda x: float(x) / 100.0
+
+    def med_p99(x):
+        return [us(np.median(x)), us(np.percentile(x, 99))]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(steps):
+            _lib_check(L.lema_debug_empty_step(P, torch.cuda.current_stream().cuda_stream))
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {
+        "clock": "s_memrealtime, 100 MHz; each reading after the item's memory operations so far",
+        "empty_graph_node_us": e0.elapsed_time(e1) / steps * 1e3,
+        "step_period_us_median": us(np.median(start[1:] - start[:-1])),
+        "step_span_us_median": us(np.median(end - start)),
+        "between_steps_us_median": us(np.median(start[1:] - end[:-1])),
+        "item_start_spread_us_median": us(np.median(t[0].max(1) - t[0].min(1))),
+        "codes_us": med_p99(t[1] - t[0]),
+        "windows_us": med_p99(t[2] - t[1]),
+        "claim_us": med_p99(t[3] - t[2]),
+        "stores_us": med_p99(t[4] - t[3]),
+        "item_total_us": med_p99(t[4] - t[0]),
+    }
+
+
+def _lib_check(status: int) -> None:
+    from latest_exact_match_attention_amd import _lib
+    _lib.check(status)
 
 
 def lm_flops_per_token(cfg) -> float:

@@ -11,6 +11,8 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "liblema_hip.so"
+# the diagnostics build (decode-step clock readings); loaded only when a caller asks for it
+STAMPS_LIB_PATH = Path(__file__).resolve().parent / "liblema_hip_stamps.so"
 
 OK, TABLE_FULL, BAD_ARG, HIP_ERROR = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
@@ -66,6 +68,21 @@ PROTOTYPES = {
 }
 
 _LIB = None
+
+
+def use_stamps_library() -> ctypes.CDLL:
+    """Load the diagnostics build in place of the product library (before any other use of
+    the library in this process): the same kernels, with the decode step's clock readings."""
+    global _LIB, LIB_PATH
+    if _LIB is not None and LIB_PATH != STAMPS_LIB_PATH:
+        raise RuntimeError("the product library is already loaded in this process")
+    LIB_PATH = STAMPS_LIB_PATH
+    L = lib()
+    L.lema_debug_step_stamps.argtypes = [_p]
+    L.lema_debug_step_stamps.restype = None
+    L.lema_debug_empty_step.argtypes = [_i64, _p]
+    L.lema_debug_empty_step.restype = ctypes.c_int
+    return L
 
 
 def lib() -> ctypes.CDLL:

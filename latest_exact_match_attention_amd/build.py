@@ -2,6 +2,11 @@
 
     python -m latest_exact_match_attention_amd.build          # compile + link
     python -m latest_exact_match_attention_amd.build --check  # is the built library current?
+    python -m latest_exact_match_attention_amd.build --stamps # diagnostics library (below)
+
+`--stamps` builds liblema_hip_stamps.so beside the product library: the same sources with the
+decode-step kernel reading the clock after each of its phases (LEMA_STEP_STAMPS), for
+`bench.py --workload decode --step-stamps`. Nothing else loads it.
 
 hipcc cross-compiles without a GPU. Objects go to `_build/` at the repository root, the
 library next to this file, where `_lib.py` loads it.
@@ -20,6 +25,7 @@ CSRC = PKG / "csrc"
 ROOT = PKG.parent
 BUILD = ROOT / "_build"
 LIB = PKG / "liblema_hip.so"
+STAMPS_LIB = PKG / "liblema_hip_stamps.so"
 INCLUDE = ROOT / "include"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -46,9 +52,9 @@ def is_current() -> bool:
     return all(p.stat().st_mtime <= t for p in _deps())
 
 
-def _compile(src: Path) -> tuple[Path, str]:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, extra: tuple = (), suffix: str = "") -> tuple[Path, str]:
+    obj = BUILD / (src.stem + suffix + ".o")
+    cmd = [HIPCC, *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     log = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                     if "packed-fp32-ops" not in l)
@@ -57,23 +63,25 @@ def _compile(src: Path) -> tuple[Path, str]:
     return obj, log
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link liblema_hip.so (always rebuilds)."""
+def build(verbose: bool = False, stamps: bool = False) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link liblema_hip.so (always rebuilds); with
+    `stamps` the diagnostics library liblema_hip_stamps.so instead."""
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
+    extra, suffix, lib = (("-DLEMA_STEP_STAMPS",), "_stamps", STAMPS_LIB) if stamps else ((), "", LIB)
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        results = list(ex.map(_compile, srcs))
+        results = list(ex.map(lambda src: _compile(src, extra, suffix), srcs))
     for _, log in results:
         if verbose and log.strip():
             print(log, file=sys.stderr)
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
            *[str(o) for o, _ in results], "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 def ensure_built() -> Path:
@@ -85,11 +93,12 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--check", action="store_true")
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--stamps", action="store_true")
     a = ap.parse_args(argv)
     if a.check:
         print("current" if is_current() else "stale")
         return 0 if is_current() else 1
-    print(build(verbose=a.verbose))
+    print(build(verbose=a.verbose, stamps=a.stamps))
     return 0
 
 

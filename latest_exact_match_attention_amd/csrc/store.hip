@@ -92,6 +92,10 @@ struct StoreArgs {
   int32_t cg_log2; // log2 of the lanes that copy one row in wave_copy_rows (pieces, up to 16)
   unsigned long long* counts;
   int32_t* full;
+#ifdef LEMA_STEP_STAMPS
+  uint64_t* stamps;    // diagnostics build: [step][item][5] realtime clock readings
+  int64_t stamp_step;
+#endif
 };
 
 __device__ __forceinline__ uint64_t code_at(const void* base, int32_t cb, int64_t i) {
@@ -313,12 +317,30 @@ __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, con
 // enough (`spec`), so a hit needs no further read; after the windows only a claim (one CAS)
 // is still a round trip. The query is answered before the key touches the table: a hit's value
 // is stored to `out` (its load complete) before any store into the table is issued.
+//
+// The diagnostics build (LEMA_STEP_STAMPS, `build --stamps`) reads the GPU's constant 100 MHz
+// clock at five points of each item -- start, codes loaded, first windows read, claim done,
+// value and count written -- each after waiting for the item's memory operations so far,
+// into a buffer set with lema_debug_step_stamps. The product build has none of it.
+#ifdef LEMA_STEP_STAMPS
+#define STEP_STAMP(k)                                                                  \
+  do {                                                                                 \
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");                        \
+    const uint64_t t_ = __builtin_amdgcn_s_memrealtime();                              \
+    if (gl == 0 && a.stamps != nullptr) a.stamps[(a.stamp_step * a.n + i) * 5 + (k)] = t_; \
+  } while (0)
+#else
+#define STEP_STAMP(k) \
+  do {                \
+  } while (0)
+#endif
 __global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   constexpr int G = kStepGroup;
   const int64_t i = gid / G;
   const int lane = threadIdx.x & 63, gl = lane % G, gbase = lane - gl;
   if (i >= a.n) return;  // whole groups only: n is a count of items, groups are aligned
+  STEP_STAMP(0);
   const uint64_t tag = static_cast<uint64_t>(a.g0 + i) + 2;
   const bool has_q = a.qc != nullptr;
   const uint64_t kcode = code_at(a.kc, a.code_bytes, i);
@@ -328,6 +350,7 @@ __global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
   if (a.pre && gl < a.pieces) vin = *reinterpret_cast<const u32x4*>(vrow + 16 * gl);
   const int64_t khome = home_slot(kcode, tag - 2, a.cap);
   const int64_t qhome = has_q ? home_slot(qcode, tag - 2, a.cap) : 0;
+  STEP_STAMP(1);
   // the two first windows are independent: their reads are in flight together
   const Window wk = read_window<G>(a, khome, a.cap, kcode, tag, gl, gbase);
   u32x4 qval[kSpecPieces];
@@ -352,6 +375,7 @@ __global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
     }
   }
 
+  STEP_STAMP(2);
   int r;
   const int fmk = wk.match ? first_bit(wk.match) : G;
   int64_t s = -1;
@@ -363,6 +387,7 @@ __global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
     s = claim_in_window(a, kcode, tag, khome, wk.empty, gl, gbase);
     r = 1;
   }
+  STEP_STAMP(3);
   if (s >= 0) {
     uint8_t* dst = a.table + s * a.stride + 16;
     if (a.pre) {
@@ -383,6 +408,7 @@ __global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
     if (r > 0) atomicAdd(&a.counts[a.g0 + i], 1ull);
     if (r < 0) atomicOr(a.full, 1);
   }
+  STEP_STAMP(4);
 }
 
 // One sub-chunk [s0, s0 + len) of every partition, one workgroup (256 threads) per partition.
@@ -1275,6 +1301,11 @@ namespace {
 //   T = 4096: claims 597 / 558 and 846 / 659 at 512, 1236 / 1032 and 1859 / 1300 at 1024;
 //             overwrites 740 / 872 at 1024;
 //   T = 16384: bulk ahead everywhere (overwrites at 1024 partitions: 3169 / 3011).
+#ifdef LEMA_STEP_STAMPS
+uint64_t* g_stamps = nullptr;  // where the decode steps of the diagnostics build write
+int64_t g_stamp_step = 0;      // the next T == 1 exchange's row of that buffer
+#endif
+
 bool bulk_applies(int64_t P, int64_t T) {
   if (T <= 1024) return false;
   return P <= 128 || T > 2048;
@@ -1365,6 +1396,10 @@ int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, con
   a.g0 = g0;
   a.counts = reinterpret_cast<unsigned long long*>(counts);
   a.full = full;
+#ifdef LEMA_STEP_STAMPS
+  a.stamps = T == 1 ? g_stamps : nullptr;
+  a.stamp_step = a.stamps != nullptr ? g_stamp_step++ : 0;
+#endif
   const bool p16 = vbytes % 16 == 0 && aligned(table, 16) && aligned(values, 16) &&
                    (out == nullptr || aligned(out, 16));
   a.piece = p16 ? 16 : 8;
@@ -1518,3 +1553,25 @@ extern "C" int lema_store_exchange_noalloc(void* table, int64_t cap, int64_t vby
   }
   return LEMA_OK;
 }
+
+#ifdef LEMA_STEP_STAMPS
+// ---- diagnostics build only: decode-step timestamps and the graph-node floor ----
+// Every T == 1 exchange enqueued after this call (a graph capture included) writes its
+// items' five clock readings to row k of `stamps` ([steps][n][5] uint64, device memory), k
+// counting those exchanges from 0; NULL stops it.
+extern "C" void lema_debug_step_stamps(void* stamps) {
+  g_stamps = static_cast<uint64_t*>(stamps);
+  g_stamp_step = 0;
+}
+
+__global__ __launch_bounds__(kStepBlock) void empty_step_kernel(int64_t n) {
+  (void)n;
+}
+
+// A kernel with a decode step's grid for n items that does nothing: the cost of a graph node.
+extern "C" int lema_debug_empty_step(int64_t n, void* stream) {
+  const int64_t grid = (n * kStepGroup + kStepBlock - 1) / kStepBlock;
+  empty_step_kernel<<<dim3(grid), dim3(kStepBlock), 0, static_cast<hipStream_t>(stream)>>>(n);
+  return launch_status("empty_step_kernel");
+}
+#endif
