@@ -71,6 +71,14 @@ static_assert(kChunk / 64 <= 16, "word summary is a 16-bit mask");
 constexpr int kFilterWords = 256;
 constexpr int kFilterMinCodes = 512;  // used by chunks with more distinct query codes than this
 __device__ __forceinline__ uint32_t filter_hash(uint32_t h) { return (h * 0x2C1B3C6Du) >> 19; }
+// The wider filter of the queued scan (one bit per code among 32768: about 3% of the keys of
+// codes no query of the chunk carries pass it, against 12% for the 8192 bits above), and the
+// capacity of a wavefront's queue: a batch adds at most 4 * 64 keys, so a queue is looked up
+// once it holds more than kQueueCap - 256.
+constexpr int kWideBits = 32768;
+constexpr int kQueueCap = 384;
+constexpr int kScanGroup = 4;  // key batches whose loads the queued scan issues together
+__device__ __forceinline__ uint32_t wide_hash(uint32_t h) { return (h * 0x9E3779B1u) >> 17; }
 
 template <typename CodeT>
 struct ResolveLds {
@@ -86,6 +94,12 @@ struct ResolveLds {
   int32_t nq;     // distinct query codes of the chunk (the all-ones code aside)
   int32_t nneed;  // query codes that need their latest key before the chunk (summary path)
 };
+// The queued scan borrows the map (each wavefront's queue: codes in mbits, positions in mkey)
+// and the word summaries (the wide filter) before the chunk's keys fill them.
+static_assert(kMapSlots * 8 >= (kThreads / 64) * kQueueCap * 8 &&
+                  kMapSlots * 4 >= (kThreads / 64) * kQueueCap * 4 &&
+                  (kSlots + 1) * 2 >= kWideBits / 8,
+              "the queued scan's borrowed LDS");
 
 // The 4 slots of bucket b, one (u32 codes) or two (u64 codes) 16-byte LDS reads.
 template <typename CodeT>
@@ -570,12 +584,20 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
   // the code they ran before it existed.
   auto rest = [&](auto filter_on) {
     constexpr bool kFilt = decltype(filter_on)::value;
+    // Chunks with the filter scan the earlier keys first, through a wider filter, queueing the
+    // few keys that pass (see below); the map and word summaries lend it their LDS meanwhile.
+    constexpr bool kQueue = kFilt && !kSumm;
+    uint32_t* wide = reinterpret_cast<uint32_t*>(s.summ);  // kWideBits, while kQueue scans
     if constexpr (kFilt) {
 #pragma unroll
       for (int p = 0; p < kPer; ++p) {
         if (!act[p] || q[p] == SENT) continue;
         const uint32_t h = filter_hash(fold(q[p]));
         atomicOr(&s.qbits[h >> 5], 1u << (h & 31));
+        if constexpr (kQueue) {
+          const uint32_t w = wide_hash(fold(q[p]));
+          atomicOr(&wide[w >> 5], 1u << (w & 31));
+        }
       }
       bar();
     }
@@ -601,7 +623,7 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
 
     // 2a. keys inside the chunk: each sets its lane in its (code, word) mask; the key that
     // creates a (code, word) entry also sets the word's bit in the code's summary
-    {
+    auto keys_in_chunk = [&]() {
       int sl[kPer];
       find_codes(kk, sl);
 #pragma unroll
@@ -616,28 +638,125 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         if (ins)
           atomicOr(reinterpret_cast<uint32_t*>(&s.summ[sl[p] & ~1]), (1u << wd) << (16 * (sl[p] & 1)));
       }
-    }
-    // 2b. keys before the chunk raise their code's latest position. Walking backwards, a code
-    // whose latest position is already known skips the atomic, so only the first batch that
-    // holds a popular code contends on its slot.
-    for (int32_t jb = kSumm ? -1 : c0 - kBatch; jb >= 0; jb -= kPrefetch * kBatch) {
+    };
+    auto key_pos = [&](int32_t j0, int e) -> int32_t {
+      return a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
+    };
+
+    if constexpr (kQueue) {
+      // 2b (filter on). The chunk's query codes seldom repeat (more than kFilterMinCodes
+      // distinct), so few earlier keys carry one. Each earlier key is tested against a
+      // kWideBits filter of the chunk's query codes (one LDS read); the keys that pass go to
+      // their wavefront's queue, which is looked up in the query-code table in bulk, 4 keys
+      // per lane with their reads in flight together, whenever it could not take another
+      // batch and at the end. A batch then costs its loads and filter reads, and the table's
+      // dependent lookups are paid per queue rather than per batch whenever a single key of
+      // the wavefront passes. The queues live in the map's storage (codes in mbits, positions
+      // in mkey), which the in-chunk keys fill only after this scan.
+      CodeT* qcode = reinterpret_cast<CodeT*>(s.mbits) + (t >> 6) * kQueueCap;
+      int32_t* qpos = reinterpret_cast<int32_t*>(s.mkey) + (t >> 6) * kQueueCap;
+      const unsigned long long below = (1ull << lane) - 1ull;
+      int cnt = 0;  // entries in this wavefront's queue (uniform across the wavefront)
+      auto flush = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int b0 = 0; b0 < cnt; b0 += 4 * 64) {
+          CodeT c[4];
+          int32_t jj[4];
+          bool in[4];
 #pragma unroll
-      for (int d = 0; d < kPrefetch; ++d) {
-        const int32_t j0 = jb - d * kBatch;
-        if (j0 < 0) break;
-        CodeT cur[4];
+          for (int i = 0; i < 4; ++i) {
+            const int b = b0 + i * 64 + lane;
+            in[i] = b < cnt;
+            c[i] = in[i] ? qcode[b] : SENT;
+            jj[i] = in[i] ? qpos[b] : -1;
+          }
+          int sl[4];
+          find4_masked<CodeT, kBuckets>(s.code, c, SENT, in, sl);
+          int32_t known[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cur[e] = nxt[d][e];
-        if (j0 - kPrefetch * kBatch >= 0) load_batch(nxt[d], j0 - kPrefetch * kBatch);
-        int sl[4];
-        find_codes(cur, sl);
-        int32_t known[4];  // read only for keys of query codes (the others raise nothing)
+          for (int i = 0; i < 4; ++i) known[i] = sl[i] >= 0 ? s.pos[sl[i]] : 0x7FFFFFFF;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) known[e] = sl[e] >= 0 ? s.pos[sl[e]] : 0x7FFFFFFF;
+          for (int i = 0; i < 4; ++i)
+            if (sl[i] >= 0 && known[i] < jj[i]) atomicMax(&s.pos[sl[i]], jj[i]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cnt = 0;
+      };
+      // kScanGroup batches' loads are issued together and then filtered one batch after
+      // another: the filtering is too short to hide a load's latency behind one batch.
+      for (int32_t jb = c0 - kBatch; jb >= 0; jb -= kScanGroup * kBatch) {
+        CodeT grp[kScanGroup][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int32_t j = a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
-          if (sl[e] >= 0 && known[e] < j) atomicMax(&s.pos[sl[e]], j);
+        for (int g = 0; g < kScanGroup; ++g)
+          if (jb - g * kBatch >= 0) load_batch(grp[g], jb - g * kBatch);
+#pragma unroll
+        for (int g = 0; g < kScanGroup; ++g) {
+          const int32_t j0 = jb - g * kBatch;
+          if (j0 < 0) break;
+          CodeT cur[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cur[e] = grp[g][e];
+          bool pass[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w = wide_hash(fold(cur[e]));
+            pass[e] = (wide[w >> 5] >> (w & 31)) & 1u;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (cur[e] == SENT) {  // the all-ones code has its own slot, never queued
+              pass[e] = false;
+              if (sent_used && s.pos[kSlots] < key_pos(j0, e)) atomicMax(&s.pos[kSlots], key_pos(j0, e));
+            }
+            const unsigned long long bal = __ballot(pass[e]);
+            if (pass[e]) {
+              const int at = cnt + __popcll(bal & below);
+              qcode[at] = cur[e];
+              qpos[at] = key_pos(j0, e);
+            }
+            cnt += __popcll(bal);
+          }
+          if (cnt > kQueueCap - 4 * 64) flush();
+        }
+      }
+      flush();
+      bar();
+      // the map and the word summaries start over for the keys inside the chunk
+      for (int x = t; x < kMapSlots; x += kThreads) {
+        s.mkey[x] = kMapEmpty;
+        s.mbits[x] = 0;
+      }
+      for (int x = t; x <= kSlots; x += kThreads) s.summ[x] = 0;
+      bar();
+      keys_in_chunk();
+    } else {
+      keys_in_chunk();
+      // 2b. keys before the chunk raise their code's latest position. Walking backwards, a
+      // code whose latest position is already known skips the atomic, so only the first batch
+      // that holds a popular code contends on its slot.
+      for (int32_t jb = kSumm ? -1 : c0 - kBatch; jb >= 0; jb -= kPrefetch * kBatch) {
+#pragma unroll
+        for (int d = 0; d < kPrefetch; ++d) {
+          const int32_t j0 = jb - d * kBatch;
+          if (j0 < 0) break;
+          CodeT cur[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cur[e] = nxt[d][e];
+          if (j0 - kPrefetch * kBatch >= 0) load_batch(nxt[d], j0 - kPrefetch * kBatch);
+          int sl[4];
+          find_codes(cur, sl);
+          int32_t known[4];  // read only for keys of query codes (the others raise nothing)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) known[e] = sl[e] >= 0 ? s.pos[sl[e]] : 0x7FFFFFFF;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int32_t j = key_pos(j0, e);
+            if (sl[e] >= 0 && known[e] < j) atomicMax(&s.pos[sl[e]], j);
+          }
         }
       }
     }

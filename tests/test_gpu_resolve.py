@@ -506,3 +506,34 @@ def test_grouped_rows_interleaved_y(dev, T, code_dtype, alphabet):
     want_y = oracle.gather(vb, "bf16", want_src, 0)
     assert same_values(bits16(y).reshape(B * H, T, dv), want_y, "bf16")
     assert (want_src >= 0).any()
+
+
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_queued_scan_high_cardinality_rows(dev, code_dtype):
+    """Chunks whose query codes seldom repeat (more than 512 distinct: the filtered, queued
+    scan of earlier keys): queries copy keys from 1 to 15 chunks back, one hot code fills a
+    third of row 1's keys (queues overflow and are looked up many times), the all-ones code
+    appears as key and query, and row 2 has no repeats at all; every index equals the
+    oracle's, through the fused op and the resolver alone."""
+    rng = np.random.default_rng(77)
+    N, T = 3, 16384
+    hi = (1 << 40) if code_dtype == torch.int64 else 0
+    qc = rng.integers(0, 1 << 24, (N, T)) + hi
+    kc = rng.integers(0, 1 << 24, (N, T)) + hi
+    for r in range(2):
+        i = rng.integers(1024, T, 3000)
+        back = rng.integers(1, i)
+        qc[r, i] = kc[r, i - back]              # matches at every distance
+    hot = 12345 + hi
+    kc[1, rng.random(T) < 0.33] = hot
+    qc[1, rng.integers(0, T, 40)] = hot
+    kc[0, rng.integers(0, T, 50)] = -1
+    qc[0, rng.integers(0, T, 50)] = -1
+    want = oracle.latest_prev_match(qc, kc)
+    q = torch.from_numpy(qc).to(dev).to(code_dtype)
+    k = torch.from_numpy(kc).to(dev).to(code_dtype)
+    assert np.array_equal(latest_prev_match(q, k).cpu().numpy(), want)
+    v = torch.randn(1, N, T, 8, device=dev)
+    _, src = lema_from_codes(q.view(1, N, T), k.view(1, N, T), v, return_src=True)
+    assert np.array_equal(src.cpu().numpy().reshape(N, T).astype(np.int64), want)
+    assert (want[0] >= 0).sum() > 1500 and (want[1] >= 0).sum() > 1500
