@@ -63,7 +63,7 @@ class HashStore:
         self.table = torch.zeros((self.cap, self.stride), dtype=torch.uint8, device=self.device)
         self.counts_device = torch.zeros(groups, dtype=torch.int64, device=self.device)
         self.full_flag = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self._ws = None          # scratch of long calls (bulk path), grown on demand
+        self._ws = None          # scratch of long calls (bulk path), kept while small
 
     @property
     def counts(self) -> torch.Tensor:
@@ -90,7 +90,7 @@ class HashStore:
         full flag is read back (a device sync) and a full table raises like the reference;
         without it, call `check_full()` later (e.g. after a graph replay). A long call
         (T > 1024 with at most 128 partitions, T > 2048 with more) takes the bulk path with
-        a device workspace this store keeps."""
+        a device workspace, kept for the next call when at most KEEP_WORKSPACE_BYTES."""
         kc, cb = _codes(kcodes)
         n = kc.numel()
         if qcodes is not None:
@@ -125,15 +125,26 @@ class HashStore:
             out.data_ptr() if qc is not None else None, n, T, g0,
             self.counts_device.data_ptr(), self.full_flag.data_ptr(),
             ws.data_ptr() if ws is not None else None, ws_bytes, _lib.stream_of(kc)))
+        if ws is not None and ws.numel() > self.KEEP_WORKSPACE_BYTES:
+            self._ws = None       # freed once the call's kernels are done (stream-ordered)
         if check:
             self.check_full()
 
+    # Scratch of long calls above this size is handed back to torch's allocator after the call
+    # instead of being kept for the next one (a 1,024-partition prefill's is a few GB, which
+    # later decode steps do not need).
+    KEEP_WORKSPACE_BYTES = 256 << 20
+
     def _workspace(self, nbytes: int) -> torch.Tensor:
-        """Device scratch of a long call (kept for the next one; grown when too small)."""
+        """Device scratch of a long call (small ones are kept for the next call)."""
         if self._ws is None or self._ws.numel() < nbytes:
             self._ws = None
             self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         return self._ws
+
+    def release_workspace(self) -> None:
+        """Hand the kept scratch of long calls back to torch's allocator."""
+        self._ws = None
 
     def check_full(self):
         """Raise like the reference (code/lema/csrc/store.cpp:159-160) if some key since the

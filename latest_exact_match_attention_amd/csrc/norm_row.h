@@ -2,7 +2,9 @@
 // code/lema/model.py:212-255), shared by the stand-alone norm kernel and the skinny products
 // that normalise their own input, so both round every element identically:
 //   s = x (+ d), each sum rounded to bf16;
-//   h = bf16(s * rsqrt(mean(s^2) + eps) * w), the mean's sum in fp32.
+//   h = bf16(s * rsqrt(mean(s^2) + eps) * w), the mean's sum in fp32, one rounding at the end:
+//   torch's nn.RMSNorm on bf16 tensors rounds the same way (on this GPU and on the CPU), so
+//   only the order of the mean's sum can differ.
 // One wavefront per row of D elements (D % 8 == 0, D <= kNormMaxD); lane `lane` takes the
 // 8 elements at (k * 64 + lane) * 8 for each step k, and the sum of squares is added up in that
 // order and then across the wavefront.

@@ -40,9 +40,11 @@ def test_rmsnorm_matches_torch(dev, residual):
         xr = x + d if residual else x
         assert torch.equal(xo, xr)                       # the bf16 add, exactly
         want = norm(xr)
+    # torch rounds x * rsqrt(mean(x^2) + eps) * w to bf16 once, from fp32, as the kernel does;
+    # only the order of the mean's fp32 sum differs, which can move a rare element by one ulp
     rel = ((h.float() - want.float()).abs() / want.float().abs().clamp_min(1e-2)).max()
     assert rel <= 2 ** -7, rel                            # within one bf16 rounding
-    assert (h == want).float().mean() > 0.95
+    assert (h == want).float().mean() > 0.9999
 
 
 def test_cross_entropy_from_bf16_logits(dev):

@@ -580,3 +580,47 @@ def test_store_value_rows_of_8_byte_pieces(dev, d_v, dtype):
                        torch.from_numpy(v).to(dev), out, T, 0)
         assert np.array_equal(out.cpu().numpy(), ref.exchange(qc, kc, v, T, 0)), T
     assert np.array_equal(store.counts.numpy(), ref.counts())
+
+
+def _host_entries(table: torch.Tensor, vbytes: int) -> dict:
+    """(group, code) -> value bytes of a table in the reference's slot format."""
+    words = table[:, :16].contiguous().view(torch.int64)
+    live = words[:, 1] >= 2
+    g, c = (words[live, 1] - 2).tolist(), words[live, 0].tolist()
+    vals = table[live, 16:16 + vbytes].numpy()
+    return {(a, b): bytes(v) for a, b, v in zip(g, c, vals)}
+
+
+@pytest.mark.parametrize("code_dtype", [torch.int32, torch.int64])
+def test_bulk_1024_partitions_against_reference_store(dev, code_dtype):
+    """1,024 partitions x T = 4,096 (the bulk path at the partition count of a 16-stream,
+    64-head prefill), first on a fresh table where every new key claims a slot, then a second
+    call that mostly overwrites: outputs, entries and per-partition counts equal the
+    reference's own store.cpp (oracle/_ref) fed the same calls on a host table."""
+    ref = oracle.ref_store()
+    assert ref is not None, "oracle/_ref/lema_store_ref.so is not built"
+    P, T, cap = 1024, 4096, 6_000_000
+    cb = 4 if code_dtype == torch.int32 else 8
+    assert _lib.lib().lema_store_workspace_bytes(P * T, T, cb) > 0
+    rng = np.random.default_rng(1024)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    host = torch.zeros((cap, 16 + 2 * D_V), dtype=torch.uint8)
+    host_counts = torch.zeros(P, dtype=torch.int64)
+    for call in range(2):
+        qc = rng.integers(0, 3000, P * T)
+        kc = rng.integers(0, 3000, P * T)
+        v = rng.integers(-30000, 30000, size=(P * T, D_V), dtype=np.int16)
+        out = torch.empty((P * T, D_V), dtype=torch.int16, device=dev)
+        store.exchange(torch.from_numpy(qc).to(dev).to(code_dtype),
+                       torch.from_numpy(kc).to(dev).to(code_dtype), torch.from_numpy(v).to(dev),
+                       out, T, 0)
+        oh = torch.empty((P * T, D_V), dtype=torch.int16)
+        host_counts += ref.exchange(host, torch.from_numpy(qc), torch.from_numpy(kc),
+                                    torch.from_numpy(v), oh, T, 0, cap, 2 * D_V)
+        assert torch.equal(out.cpu(), oh), call
+        assert torch.equal(store.counts, host_counts), call
+    g, c, val = store.dump()
+    got = {(a, b): bytes(x) for a, b, x in
+           zip(g.cpu().tolist(), c.cpu().tolist(), val.cpu().numpy())}
+    assert got == _host_entries(host, 2 * D_V)
+    assert len(got) > 2_000_000
