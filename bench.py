@@ -114,6 +114,8 @@ def parse():
     ap.add_argument("--decode-prefill", type=int, default=262144,
                     help="keys prefilled per partition for the decode workload")
     ap.add_argument("--decode-steps", type=int, default=1024)
+    ap.add_argument("--decode-place", choices=["hbm", "ram"], default="hbm",
+                    help="decode: the store table in device memory or in pinned host RAM")
     ap.add_argument("--step-stamps", action="store_true",
                     help="decode: run the diagnostics build (build --stamps), whose step kernel "
                          "reads the clock after each phase, and report the breakdown and the "
@@ -296,7 +298,8 @@ def bench_decode(a):
     vbytes = dv * 2
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(0)
-    store = HashStore(dv, groups=P, dtype=torch.bfloat16, capacity=cap, device=dev)
+    store = HashStore(dv, groups=P, dtype=torch.bfloat16, capacity=cap, device=dev,
+                      place=a.decode_place)
     ref = None
     if not a.no_cpu_baseline:
         import oracle
@@ -405,6 +408,7 @@ def bench_decode(a):
         "data": "synthetic (torch device RNG: uniform 32-bit codes, N(0,1) values)",
         "config": {"workload": "decode", "partitions": P, "sequences": seqs, "heads": heads,
                    "d_v": dv, "prefilled_per_partition": n0, "capacity": cap,
+                   "table_place": a.decode_place,
                    "table_bytes": cap * (16 + vbytes), "load_after": round(store.load(), 4),
                    "graph": f"{steps} steps in one HIP graph", "hit_rate": hits,
                    "parallelism": "single GPU"},

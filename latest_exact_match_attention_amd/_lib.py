@@ -6,6 +6,7 @@ been built, `lib()` raises and names the build command.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from pathlib import Path
 
 import torch
@@ -116,6 +117,64 @@ def check(status: int) -> None:
 def stream_of(t: torch.Tensor) -> int:
     """The raw hipStream_t of the current torch stream on t's device."""
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+# ---- host memory the GPU works on in place (a store table in host RAM) ----
+# The HIP runtime this process already uses (torch's; the library links the same soname).
+_HIP = None
+HIP_HOST_MALLOC_COHERENT = 0x40000000        # hipHostMallocCoherent
+HIP_ATTR_HOST_NATIVE_ATOMIC = 15             # hipDeviceAttributeHostNativeAtomicSupported
+
+
+def hip_runtime() -> ctypes.CDLL:
+    global _HIP
+    if _HIP is None:
+        torch.cuda.init()
+        H = ctypes.CDLL("libamdhip64.so.7")
+        H.hipHostMalloc.argtypes = [ctypes.POINTER(_p), ctypes.c_size_t, ctypes.c_uint]
+        H.hipHostFree.argtypes = [_p]
+        H.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(_p), _p, ctypes.c_uint]
+        H.hipDeviceGetAttribute.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                            ctypes.c_int]
+        for f in ("hipHostMalloc", "hipHostFree", "hipHostGetDevicePointer",
+                  "hipDeviceGetAttribute"):
+            getattr(H, f).restype = ctypes.c_int
+        _HIP = H
+    return _HIP
+
+
+def host_atomics_supported(device: int) -> bool:
+    """Whether the link between `device` and the host carries the device's atomic operations
+    on host memory (a claim in a host-RAM table is a 64-bit compare-and-swap)."""
+    v = ctypes.c_int(0)
+    rc = hip_runtime().hipDeviceGetAttribute(ctypes.byref(v), HIP_ATTR_HOST_NATIVE_ATOMIC,
+                                             device)
+    return rc == 0 and v.value == 1
+
+
+class HostTable:
+    """`nbytes` of zeroed, pinned, coherent host memory that the GPU reads, writes and updates
+    atomically in place (no copies), freed with the object. `tensor()` views it from the CPU;
+    `dev_ptr` is the address kernels use."""
+
+    def __init__(self, nbytes: int):
+        H = hip_runtime()
+        ptr = _p()
+        rc = H.hipHostMalloc(ctypes.byref(ptr), max(1, nbytes), HIP_HOST_MALLOC_COHERENT)
+        if rc != 0 or not ptr.value:
+            raise RuntimeError(f"hipHostMalloc of {nbytes} bytes failed (status {rc})")
+        self.ptr, self.nbytes = ptr.value, nbytes
+        self._finalizer = weakref.finalize(self, H.hipHostFree, ptr.value)
+        ctypes.memset(self.ptr, 0, nbytes)
+        dev = _p()
+        rc = H.hipHostGetDevicePointer(ctypes.byref(dev), ptr.value, 0)
+        if rc != 0 or not dev.value:
+            raise RuntimeError(f"hipHostGetDevicePointer failed (status {rc})")
+        self.dev_ptr = dev.value
+        self._buf = (ctypes.c_uint8 * nbytes).from_address(self.ptr)
+
+    def tensor(self) -> torch.Tensor:
+        return torch.frombuffer(self._buf, dtype=torch.uint8)
 
 
 def widen_codes(t: torch.Tensor) -> torch.Tensor:

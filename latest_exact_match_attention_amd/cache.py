@@ -43,13 +43,19 @@ class HashStore:
     head) partition; an entry's key is (group, code) (code/lema/cache.py:129-201).
 
     `capacity` is slots, exact (the home slot is a multiply, not a mask). The table is a zeroed
-    device allocation -- zero is the free state, so it is empty as allocated -- of
+    allocation -- zero is the free state, so it is empty as allocated -- of
     capacity x (16 + d_v * itemsize) bytes, never resized; a key that finds no free slot makes
     `exchange` raise RuntimeError("hash table full ...").
+
+    `place` puts the table in device memory ("hbm") or in pinned host RAM ("ram", the
+    reference's placement, for tables larger than device memory): the same kernels then read,
+    write and claim slots in host memory over the host link, in place. "ram" needs a link that
+    carries the device's atomics to host memory, and is refused otherwise. Codes, values, counts
+    and the full flag stay on the device either way.
     """
 
     def __init__(self, d_v: int, groups: int, dtype=np.float16, capacity: int = 256,
-                 device=None):
+                 device=None, place: str = "hbm"):
         self.d_v, self.dtype, self.groups = d_v, dtype, groups
         self.vbytes = d_v * _itemsize(dtype)
         if self.vbytes % 8:
@@ -60,7 +66,21 @@ class HashStore:
         self.device = torch.device(device) if device is not None else torch.device("cuda", 0)
         if self.device.type != "cuda":
             raise TypeError(f"the store lives in device memory; got device {self.device}")
-        self.table = torch.zeros((self.cap, self.stride), dtype=torch.uint8, device=self.device)
+        if place not in ("hbm", "ram"):
+            raise ValueError(f"place must be 'hbm' (device memory) or 'ram' (host memory), "
+                             f"got {place!r}")
+        self.place = place
+        self._host = None
+        if place == "ram":
+            dev_index = self.device.index if self.device.index is not None else 0
+            if not _lib.host_atomics_supported(dev_index):
+                raise RuntimeError("a store in host RAM needs device atomics on host memory, "
+                                   "which this system's host link does not carry")
+            self._host = _lib.HostTable(self.cap * self.stride)
+            self.table = self._host.tensor().view(self.cap, self.stride)
+        else:
+            self.table = torch.zeros((self.cap, self.stride), dtype=torch.uint8,
+                                     device=self.device)
         self.counts_device = torch.zeros(groups, dtype=torch.int64, device=self.device)
         self.full_flag = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._ws = None          # scratch of long calls (bulk path), kept while small
@@ -120,7 +140,7 @@ class HashStore:
         ws_bytes = L.lema_store_workspace_bytes(n, T, cb)
         ws = self._workspace(ws_bytes) if ws_bytes > 0 else None
         _lib.check(L.lema_store_exchange_ws(
-            self.table.data_ptr(), self.cap, self.vbytes,
+            self.table_ptr(), self.cap, self.vbytes,
             qc.data_ptr() if qc is not None else None, kc.data_ptr(), cb, values.data_ptr(),
             out.data_ptr() if qc is not None else None, n, T, g0,
             self.counts_device.data_ptr(), self.full_flag.data_ptr(),
@@ -134,6 +154,10 @@ class HashStore:
     # instead of being kept for the next one (a 1,024-partition prefill's is a few GB, which
     # later decode steps do not need).
     KEEP_WORKSPACE_BYTES = 256 << 20
+
+    def table_ptr(self) -> int:
+        """The table's address for the kernels (the device-side address of a host table)."""
+        return self._host.dev_ptr if self._host is not None else self.table.data_ptr()
 
     def _workspace(self, nbytes: int) -> torch.Tensor:
         """Device scratch of a long call (small ones are kept for the next call)."""
@@ -155,8 +179,11 @@ class HashStore:
             raise RuntimeError(_lib.FULL_MESSAGE)
 
     def dump(self):
-        """The published entries as device tensors (group, code, value rows): the table read
-        the way code/experiments/app_retrieval/fixedpoint.py:72-82 reads the reference's."""
+        """The published entries (group, code, value rows), on the table's side (host tensors
+        for a table in RAM): the table read the way
+        code/experiments/app_retrieval/fixedpoint.py:72-82 reads the reference's."""
+        if self._host is not None:
+            torch.cuda.synchronize(self.device)   # the kernels write host memory in place
         words = self.table[:, :16].contiguous().view(torch.int64).view(self.cap, 2)
         state = words[:, 1]
         live = state >= 2
@@ -189,14 +216,14 @@ class LayerStore:
 
 
 class LemaCache:
-    """The retrieval state of a model: one shared HBM table, viewed per layer
-    (code/lema/cache.py:305-378). Sized once: `capacity` slots, or
-    ceil(depth * batch * heads * max_cache_len / max_load) for the worst case of one new code
-    per token per head; it never resizes."""
+    """The retrieval state of a model: one shared table, viewed per layer
+    (code/lema/cache.py:305-378), in device memory (place "hbm") or host RAM ("ram"). Sized
+    once: `capacity` slots, or ceil(depth * batch * heads * max_cache_len / max_load) for the
+    worst case of one new code per token per head; it never resizes."""
 
     def __init__(self, cfg, dtype=torch.bfloat16, pin: bool = True, max_cache_len: int = 8192,
                  max_load: float = 0.7, batch: int = 1, capacity: int | None = None,
-                 codes_hook=None, device=None):
+                 codes_hook=None, device=None, place: str = "hbm"):
         if dtype not in (torch.float32, torch.float16, torch.bfloat16):
             raise ValueError(f"cache dtype must be one of "
                              f"{[torch.float32, torch.float16, torch.bfloat16]}, got {dtype}")
@@ -207,7 +234,7 @@ class LemaCache:
                                                          / max_load)
         self.cfg, self.batch, self.dtype = cfg, batch, dtype
         self.store = HashStore(cfg.d_v, groups=cfg.depth * P, dtype=dtype, capacity=slots,
-                               device=device)
+                               device=device, place=place)
         self.t = 0
         self.codes_hook = codes_hook
         self._views = [LayerStore(self.store, i * P, P, codes_hook, i) for i in range(cfg.depth)]

@@ -66,7 +66,7 @@ class LemaDecoder:
         if not model.lema_layers() or not all(a.hard for a in model.lema_layers()):
             raise ValueError("LemaDecoder needs an all-LEMA model in hard mode")
         if not isinstance(cache, LemaCache):
-            raise TypeError("LemaDecoder needs a device LemaCache (model.new_cache('hbm'))")
+            raise TypeError("LemaDecoder needs a LemaCache of this package (model.new_cache())")
         self.model, self.cache = model, cache
         B, L = cache.batch, cfg.depth
         dev = next(model.parameters()).device

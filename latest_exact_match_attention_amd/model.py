@@ -417,17 +417,20 @@ class Transformer(nn.Module):
             att.hard = hard
 
     def new_cache(self, place: str = "hbm", **kw):
-        """A retrieval cache for this model in device memory (the reference's host-RAM cache,
-        code/lema/model.py:306-324, moved to HBM): `max_cache_len=` or `capacity=` slots,
-        `batch=`, `max_load=`, `codes_hook=` as in `LemaCache`."""
+        """A retrieval cache for this model (code/lema/model.py:306-324): in device memory
+        (place "hbm", or "vram"), or in pinned host RAM ("ram", the reference's placement,
+        for caches larger than device memory; the same kernels work on it in place over the
+        host link). `max_cache_len=` or `capacity=` slots, `batch=`, `max_load=`,
+        `codes_hook=` as in `LemaCache`."""
         from .cache import LemaCache
-        if place not in ("hbm", "vram"):
-            raise ValueError(f"a LEMA cache here lives in device memory (place='hbm'); "
-                             f"place={place!r} is not an implementation of it")
+        if place not in ("hbm", "vram", "ram"):
+            raise ValueError(f"a LEMA cache lives in device memory (place='hbm') or host RAM "
+                             f"(place='ram'); place={place!r} is not an implementation of it")
         p = next(self.parameters())
         kw.setdefault("dtype", p.dtype)
         kw.pop("pin", None)
-        return LemaCache(self.cfg, device=p.device, **kw)
+        return LemaCache(self.cfg, device=p.device, place="ram" if place == "ram" else "hbm",
+                         **kw)
 
     def forward(self, idx, *, cache=None, return_logits=True):
         """Run `idx` through the model (code/lema/model.py:337-363).

@@ -203,3 +203,27 @@ def test_model_matches_reference_fixture(dev, name):
     assert abs(loss - ref) <= 1e-5 * abs(ref), (loss, ref)
     assert abs(ours - ref) <= 1e-5 * abs(ref), (ours, ref)
     assert np.abs(logits.float().cpu().numpy() - g[f"{name}/logits"]).max() <= 1e-3
+
+
+def test_cache_in_host_ram_equals_dense_and_decodes_in_a_graph(dev):
+    """A model cache in host RAM (new_cache("ram")): fed in chunks of 16 it gives the dense
+    forward, and the single-graph decoder's steps equal eager steps on an HBM cache."""
+    m, cfg = make(dev, **GEOS["d4"])
+    x = torch.randint(0, 64, (2, 64), device=dev)
+    with torch.no_grad():
+        dense = m(x)
+        cache = m.new_cache("ram", max_cache_len=64 + 8, batch=2)
+        assert cache.store.place == "ram"
+        parts = [m(x[:, s:s + 16], cache=cache) for s in range(0, 64, 16)]
+        assert torch.equal(torch.cat(parts, dim=1).argmax(-1), dense.argmax(-1))
+        assert (torch.cat(parts, dim=1) - dense).abs().max() < 1e-4
+        ref = m.new_cache("hbm", max_cache_len=64 + 8, batch=2)
+        m(x, cache=ref, return_logits=False)
+        dec = decoder(m, cache, tok=x[:, -1:])
+        tok = x[:, -1:].clone()
+        for _ in range(6):
+            want = m(tok, cache=ref).argmax(-1)
+            got = dec.step().clone()
+            assert torch.equal(got, want)
+            tok = want
+        assert cache.entries() == ref.entries()

@@ -18,10 +18,12 @@ GOLDEN = Path(__file__).resolve().parent / "golden"
 D_V = 8                                   # uint16 rows: 16 bytes, as the reference test
 
 
-def run_dict_case(dev, seed, P, T, chunk, n_codes, capacity, code_dtype=torch.int64):
-    """code/tests/test_store.py:17-41 against the HBM store."""
+def run_dict_case(dev, seed, P, T, chunk, n_codes, capacity, code_dtype=torch.int64,
+                  place="hbm"):
+    """code/tests/test_store.py:17-41 against the store (table in HBM or host RAM)."""
     rng = np.random.default_rng(seed)
-    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=capacity, device=dev)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=capacity, device=dev,
+                      place=place)
     ref = oracle.DictStore(P, 2 * D_V)
     codes = rng.integers(0, n_codes, size=(2, P, T), dtype=np.int64) * 7919 % (n_codes + 2)
     vals = rng.integers(0, 1 << 16, size=(P, T, D_V), dtype=np.uint16)
@@ -95,17 +97,38 @@ def test_store_short_long_call_few_partitions(dev):
                   code_dtype=torch.int32)
 
 
+@pytest.mark.parametrize("T,chunk,P", [(300, 1, 64), (2000, 500, 200), (3000, 3000, 16)])
+def test_store_in_host_ram(dev, T, chunk, P):
+    """The table in pinned host RAM (the reference's placement), worked on in place by the
+    same kernels over the host link: decode-sized steps, chunked calls and a bulk call equal
+    the dict, entries included, and the table is the host tensor the CPU reads."""
+    store, ref = run_dict_case(dev, seed=T, P=P, T=T, chunk=chunk, n_codes=300,
+                               capacity=200_000, place="ram")
+    assert store.place == "ram" and not store.table.is_cuda
+    grp, code, val = store.dump()
+    got = {(int(a), int(b)): bytes(c) for a, b, c in zip(grp.numpy(), code.numpy(), val.numpy())}
+    assert got == {(p, k): bytes(v) for p, d in enumerate(ref.ref) for k, v in d.items()}
+
+
+def test_store_in_host_ram_overfull_raises(dev):
+    with pytest.raises(RuntimeError, match="full"):
+        run_dict_case(dev, seed=3, P=50, T=100, chunk=100, n_codes=100, capacity=1000,
+                      place="ram")
+
+
 def test_store_overfull_raises(dev):
     with pytest.raises(RuntimeError, match="full"):
         run_dict_case(dev, seed=3, P=50, T=100, chunk=100, n_codes=100, capacity=1000)
 
 
-def test_store_contended_decode(dev):
+@pytest.mark.parametrize("place", ["hbm", "ram"])
+def test_store_contended_decode(dev, place):
     """1024 partitions claiming slots of a small shared table every step (load ~0.9 at the
-    end): concurrent claims from every XCD must never hand one slot to two keys."""
+    end): concurrent claims from every XCD must never hand one slot to two keys, in device
+    memory and in host RAM."""
     P, steps, cap = 1024, 60, 70_000
     rng = np.random.default_rng(9)
-    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    store = HashStore(D_V, groups=P, dtype=np.uint16, capacity=cap, device=dev, place=place)
     ref = oracle.DictStore(P, 2 * D_V)
     for s in range(steps):
         qc = rng.integers(0, 2**63, P, dtype=np.int64)

@@ -70,8 +70,8 @@ def test_forward_refuses_cpu_and_soft_mode():
     m.set_hard(True)
     with pytest.raises(TypeError):
         m(torch.zeros(1, 4, dtype=torch.long))        # the exact op is device-only
-    with pytest.raises(ValueError, match="device memory"):
-        m.new_cache("ram")
+    with pytest.raises(ValueError, match="host RAM"):
+        m.new_cache("disk")
 
 
 def test_model_oracle_exact_op_is_the_dict_rule():
