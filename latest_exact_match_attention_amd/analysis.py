@@ -30,7 +30,7 @@ def trace(model, x, reduce=None, return_logits=True):
 
     def hook(li):
         def fn(blk, inp, _out):
-            zq, zk, _ = blk.attn.project(blk.norm1(inp[0]))
+            zq, zk, _ = blk.attn.project(blk.pre_attn(inp[0]))
             qc, kc = pack_codes(zq), pack_codes(zk)
             B, H, T = qc.shape
             src = latest_prev_match(qc.reshape(B * H, T), kc.reshape(B * H, T))

@@ -14,9 +14,11 @@ block norm1, q, k, v, o, norm2, gate, up, down, then norm_f, lm_head; Gaussian s
 outputs scaled by 1/sqrt(2 * depth): code/lema/model.py:258-281), so the same seed gives the
 same weights.
 
-In bf16 on the GPU the SwiGLU product, the attention residual add with the MLP's pre-norm, the
-final norm and the loss run as fused HIP kernels (the reference compiles these segments with
-torch.compile). The attention pre-norm, whose output decides the codes, stays torch's RMSNorm.
+In bf16 on the GPU the SwiGLU product, both pre-norms (the MLP's with the attention residual
+add), the final norm and the loss run as fused HIP kernels (the reference compiles these
+segments with torch.compile). The norm kernel rounds like torch's RMSNorm (one rounding of
+x * rstd * w from fp32), so the codes, the signs of the attention input's projections, stay
+the ones torch's norm gives.
 
 Only the hard (exact) op is implemented: the training surrogate (stick-breaking relaxation,
 straight-through binarization) and the softmax / gated-deltanet baselines are not part of the
@@ -350,11 +352,17 @@ class Block(nn.Module):
         self.mlp = SwiGLU(cfg.dim, cfg.dim_ff)
         self.seg = None
 
+    def pre_attn(self, x):
+        """The attention's input norm1(x): in bf16 on the device the fused norm kernel, which
+        rounds x * rsqrt(mean(x^2) + eps) * w once from fp32 as torch's RMSNorm does (the
+        codes are the signs of its projections)."""
+        return rms_norm(x, self.norm1)[0]
+
     def gpu_pre(self, x):
         """Normalise, project, pack both codes (code/lema/model.py:224-227). On decode shapes
         the three projections are one launch, q and k going straight to codes (skinny MFMA
         kernel, pack epilogues)."""
-        h = self.norm1(x)
+        h = self.pre_attn(x)
         at, c = self.attn, self.attn.cfg
         ct = code_dtype_for(c.d_qk)
         fused = project_qkv(h, at, ct)
@@ -384,7 +392,7 @@ class Block(nn.Module):
             pre, post = self.seg or (self.gpu_pre, self.gpu_post)
             qc, kc, v = pre(x)
             return post(x, store.exchange(qc, kc, v))
-        h, x = rms_norm(x, self.norm2, self.attn(self.norm1(x)))
+        h, x = rms_norm(x, self.norm2, self.attn(self.pre_attn(x)))
         return self.mlp(h, residual=x)
 
 
