@@ -93,6 +93,7 @@ struct ResolveLds {
   int32_t sent_used;
   int32_t nq;     // distinct query codes of the chunk (the all-ones code aside)
   int32_t nneed;  // query codes that need their latest key before the chunk (summary path)
+  int32_t khit;   // some key of the chunk carries a query code of the chunk (queued scan)
 };
 // The queued scan borrows the map (each wavefront's queue: codes in mbits, positions in mkey)
 // and the word summaries (the wide filter) before the chunk's keys fill them.
@@ -555,6 +556,7 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
     s.sent_used = 0;
     s.nq = 0;
     s.nneed = 0;
+    s.khit = 0;
   }
   bar();
 
@@ -643,6 +645,7 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       return a.kvec ? j0 + 4 * t + e : j0 + e * kThreads + t;
     };
 
+    bool fast = false;  // (queued scan) no key of the chunk carries a query code of it
     if constexpr (kQueue) {
       // 2b (filter on). The chunk's query codes seldom repeat (more than kFilterMinCodes
       // distinct), so few earlier keys carry one. Each earlier key is tested against a
@@ -724,15 +727,30 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         }
       }
       flush();
-      bar();
-      // the map and the word summaries start over for the keys inside the chunk
-      for (int x = t; x < kMapSlots; x += kThreads) {
-        s.mkey[x] = kMapEmpty;
-        s.mbits[x] = 0;
+      // Does some key of the chunk carry a query code of the chunk? Codes that seldom repeat
+      // usually give none (C5's layers: ~97% of chunks), and then no query has an in-chunk
+      // match: every answer is the code's latest position before the chunk, and the map, the
+      // chunk's own keys and the per-query map lookups are skipped.
+      {
+        int sl[kPer];
+        find_codes(kk, sl);
+        bool hit = false;
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) hit = hit || (act[p] && sl[p] >= 0);
+        if (__ballot(hit) != 0 && lane == 0) s.khit = 1;
       }
-      for (int x = t; x <= kSlots; x += kThreads) s.summ[x] = 0;
       bar();
-      keys_in_chunk();
+      fast = s.khit == 0;
+      if (!fast) {
+        // the map and the word summaries start over for the keys inside the chunk
+        for (int x = t; x < kMapSlots; x += kThreads) {
+          s.mkey[x] = kMapEmpty;
+          s.mbits[x] = 0;
+        }
+        for (int x = t; x <= kSlots; x += kThreads) s.summ[x] = 0;
+        bar();
+        keys_in_chunk();
+      }
     } else {
       keys_in_chunk();
       // 2b. keys before the chunk raise their code's latest position. Walking backwards, a
@@ -760,12 +778,18 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         }
       }
     }
-    bar();
+    if (!fast) bar();
 
     // 3. resolve: the latest earlier lane of the own word, else the latest earlier word of the
     // chunk holding the code, else the latest position before the chunk
     bool nb[kPer];  // the answer is the code's latest position before the chunk
-    {
+    if (fast) {
+#pragma unroll
+      for (int p = 0; p < kPer; ++p) {
+        nb[p] = act[p];
+        src[p] = act[p] ? s.pos[qs[p]] : -1;
+      }
+    } else {
       int m[kPer];
       uint32_t key[kPer];
 #pragma unroll

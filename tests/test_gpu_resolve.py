@@ -513,8 +513,9 @@ def test_queued_scan_high_cardinality_rows(dev, code_dtype):
     """Chunks whose query codes seldom repeat (more than 512 distinct: the filtered, queued
     scan of earlier keys): queries copy keys from 1 to 15 chunks back, one hot code fills a
     third of row 1's keys (queues overflow and are looked up many times), the all-ones code
-    appears as key and query, and row 2 has no repeats at all; every index equals the
-    oracle's, through the fused op and the resolver alone."""
+    appears as key and query, row 2 has no repeats at all and row 3 repeats only keys of
+    earlier chunks; every index equals the oracle's, through the fused op and the resolver
+    alone."""
     rng = np.random.default_rng(77)
     N, T = 3, 16384
     hi = (1 << 40) if code_dtype == torch.int64 else 0
@@ -529,7 +530,28 @@ def test_queued_scan_high_cardinality_rows(dev, code_dtype):
     qc[1, rng.integers(0, T, 40)] = hot
     kc[0, rng.integers(0, T, 50)] = -1
     qc[0, rng.integers(0, T, 50)] = -1
+    # row 3: queries copy keys of earlier chunks only, so its chunks answer from before
+    # themselves alone
+    q3 = rng.integers(0, 1 << 24, (1, T)) + hi
+    k3 = rng.integers(0, 1 << 24, (1, T)) + hi
+    i = rng.integers(1024, T, 4000)
+    q3[0, i] = k3[0, rng.integers(0, i - i % 1024)]
+    qc, kc = np.concatenate([qc, q3]), np.concatenate([kc, k3])
+    N = 4
     want = oracle.latest_prev_match(qc, kc)
+    # Both kinds of filtered chunk are present: chunks none of whose keys carries one of their
+    # query codes (answered from before the chunk alone, without the key map), among them
+    # chunks with answers from earlier chunks, and chunks with in-chunk matches.
+    kinds = {"keyless": 0, "keyless_answered": 0, "in_chunk": 0}
+    for r in range(N):
+        for c0 in range(0, T, 1024):
+            shared = np.intersect1d(qc[r, c0:c0 + 1024], kc[r, c0:c0 + 1024]).size > 0
+            if not shared:
+                kinds["keyless"] += 1
+                kinds["keyless_answered"] += int((want[r, c0:c0 + 1024] >= 0).any())
+            elif (want[r, c0:c0 + 1024] >= c0).any():
+                kinds["in_chunk"] += 1
+    assert all(n > 0 for n in kinds.values()), kinds
     q = torch.from_numpy(qc).to(dev).to(code_dtype)
     k = torch.from_numpy(kc).to(dev).to(code_dtype)
     assert np.array_equal(latest_prev_match(q, k).cpu().numpy(), want)
