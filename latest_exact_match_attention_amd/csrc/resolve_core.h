@@ -594,11 +594,12 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
 #pragma unroll
       for (int p = 0; p < kPer; ++p) {
         if (!act[p] || q[p] == SENT) continue;
-        const uint32_t h = filter_hash(fold(q[p]));
-        atomicOr(&s.qbits[h >> 5], 1u << (h & 31));
-        if constexpr (kQueue) {
+        if constexpr (kQueue) {  // the wide filter serves the chunk's own keys too
           const uint32_t w = wide_hash(fold(q[p]));
           atomicOr(&wide[w >> 5], 1u << (w & 31));
+        } else {
+          const uint32_t h = filter_hash(fold(q[p]));
+          atomicOr(&s.qbits[h >> 5], 1u << (h & 31));
         }
       }
       bar();
@@ -611,8 +612,13 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         bool pass[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t h = filter_hash(fold(c[i]));
-          pass[i] = (s.qbits[h >> 5] >> (h & 31)) & 1u;
+          if constexpr (kQueue) {  // only before the map takes the wide filter's storage back
+            const uint32_t w = wide_hash(fold(c[i]));
+            pass[i] = (wide[w >> 5] >> (w & 31)) & 1u;
+          } else {
+            const uint32_t h = filter_hash(fold(c[i]));
+            pass[i] = (s.qbits[h >> 5] >> (h & 31)) & 1u;
+          }
         }
         find4_masked<CodeT, kBuckets>(s.code, c, SENT, pass, sl);
       } else {
@@ -625,9 +631,7 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
 
     // 2a. keys inside the chunk: each sets its lane in its (code, word) mask; the key that
     // creates a (code, word) entry also sets the word's bit in the code's summary
-    auto keys_in_chunk = [&]() {
-      int sl[kPer];
-      find_codes(kk, sl);
+    auto keys_in_chunk = [&](const int (&sl)[kPer]) {
 #pragma unroll
       for (int p = 0; p < kPer; ++p) {
         if (!act[p] || sl[p] < 0) continue;
@@ -731,14 +735,12 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       // usually give none (C5's layers: ~97% of chunks), and then no query has an in-chunk
       // match: every answer is the code's latest position before the chunk, and the map, the
       // chunk's own keys and the per-query map lookups are skipped.
-      {
-        int sl[kPer];
-        find_codes(kk, sl);
-        bool hit = false;
+      int sl[kPer];
+      find_codes(kk, sl);
+      bool hit = false;
 #pragma unroll
-        for (int p = 0; p < kPer; ++p) hit = hit || (act[p] && sl[p] >= 0);
-        if (__ballot(hit) != 0 && lane == 0) s.khit = 1;
-      }
+      for (int p = 0; p < kPer; ++p) hit = hit || (act[p] && sl[p] >= 0);
+      if (__ballot(hit) != 0 && lane == 0) s.khit = 1;
       bar();
       fast = s.khit == 0;
       if (!fast) {
@@ -749,10 +751,14 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         }
         for (int x = t; x <= kSlots; x += kThreads) s.summ[x] = 0;
         bar();
-        keys_in_chunk();
+        keys_in_chunk(sl);
       }
     } else {
-      keys_in_chunk();
+      {
+        int sl[kPer];
+        find_codes(kk, sl);
+        keys_in_chunk(sl);
+      }
       // 2b. keys before the chunk raise their code's latest position. Walking backwards, a
       // code whose latest position is already known skips the atomic, so only the first batch
       // that holds a popular code contends on its slot.
