@@ -801,15 +801,32 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
 #pragma unroll
       for (int p = 0; p < kPer; ++p)
         key[p] = (static_cast<uint32_t>(qs[p]) << 4) | ((p * kThreads + t) >> 6);
-      find4<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty, m);
       uint64_t bits[kPer];
       uint32_t words[kPer];
       int32_t before[kPer];
+      if constexpr (kFilt) {
+        // Codes that seldom repeat: most queries' codes have no key in the chunk, which
+        // their word summary (read first) shows; only the others look up their lane mask.
+        bool own[kPer];
 #pragma unroll
-      for (int p = 0; p < kPer; ++p) {  // every read a position may need, issued together
-        bits[p] = s.mbits[m[p] >= 0 ? m[p] : 0];
-        words[p] = s.summ[qs[p]];
-        before[p] = s.pos[qs[p]];
+        for (int p = 0; p < kPer; ++p) {
+          words[p] = s.summ[qs[p]];
+          before[p] = s.pos[qs[p]];
+        }
+#pragma unroll
+        for (int p = 0; p < kPer; ++p)
+          own[p] = act[p] && ((words[p] >> ((p * kThreads + t) >> 6)) & 1u);
+        find4_masked<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty, own, m);
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) bits[p] = m[p] >= 0 ? s.mbits[m[p]] : 0;
+      } else {
+        find4<uint32_t, kMapBuckets>(s.mkey, key, kMapEmpty, m);
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {  // every read a position may need, issued together
+          bits[p] = s.mbits[m[p] >= 0 ? m[p] : 0];
+          words[p] = s.summ[qs[p]];
+          before[p] = s.pos[qs[p]];
+        }
       }
       uint32_t key2[kPer];
       bool second[kPer];
@@ -836,7 +853,7 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
         }
       }
       int m2[kPer];
-      find4<uint32_t, kMapBuckets>(s.mkey, key2, kMapEmpty, m2);
+      find4_masked<uint32_t, kMapBuckets>(s.mkey, key2, kMapEmpty, second, m2);
 #pragma unroll
       for (int p = 0; p < kPer; ++p)
         if (second[p]) src[p] += 63 - __clzll(s.mbits[m2[p]]);
