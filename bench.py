@@ -221,7 +221,9 @@ def bench_prefill(a):
     hits = float((src >= 0).float().mean().item())
     nq = B * H * T
     achieved = BYTES_PER_QUERY * nq / (ms * 1e-3) / 1e9
-    copy_gbps = measured_copy_gbps(vd, y, stream)  # after the timed region; overwrites y
+    # after the timed region; both overwrite y
+    copy_gbps = measured_copy_gbps(vd, y, stream, lib_copy=True)
+    torch_copy_gbps = measured_copy_gbps(vd, y, stream)
     cpu = None if a.no_cpu_baseline else cpu_baseline_prefill(qc, kc, v32, a.cpu_rows)
     return {
         "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
@@ -246,25 +248,36 @@ def bench_prefill(a):
                      "kernel": "resolve_kernel (fused resolve + gather)",
                      "bytes_per_query": BYTES_PER_QUERY, "queries_per_launch": nq,
                      "copy_measured": {"GBps": copy_gbps, "frac": achieved / copy_gbps,
-                                       "what": "device copy of the value tensor (read + write "
-                                               f"{2 * vd.numel() * vd.element_size()} bytes), "
-                                               "HIP events, median of 20"}},
+                                       "what": "lema_device_copy of the value tensor (read + "
+                                               f"write {2 * vd.numel() * vd.element_size()} "
+                                               "bytes), HIP events, median of 20",
+                                       "torch_copy_GBps": torch_copy_gbps}},
         "cpu_baseline": cpu,
     }
 
 
-def measured_copy_gbps(src, dst, stream, reps: int = 20) -> float:
-    """A plain device copy's rate on this GPU (bytes read + written per second, GB/s): the
-    streaming rate HBM actually reaches, beside the 8 TB/s specification."""
+def measured_copy_gbps(src, dst, stream, reps: int = 20, lib_copy: bool = False) -> float:
+    """A device copy's rate on this GPU (bytes read + written per second, GB/s): the streaming
+    rate HBM actually reaches, beside the 8 TB/s specification. lib_copy: the library's
+    lema_device_copy (consecutive workgroups on consecutive 32 KB regions), else torch's."""
     import torch
+    from latest_exact_match_attention_amd import _lib
+    nbytes = src.numel() * src.element_size()
+
+    def run():
+        if lib_copy:
+            _lib.check(_lib.lib().lema_device_copy(src.data_ptr(), dst.data_ptr(), nbytes,
+                                                   stream.cuda_stream))
+        else:
+            dst.copy_(src)
     for _ in range(3):
-        dst.copy_(src)
+        run()
     torch.cuda.synchronize()
     times = []
     for _ in range(reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        dst.copy_(src)
+        run()
         e1.record(stream)
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1))

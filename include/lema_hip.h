@@ -38,6 +38,11 @@ enum lema_miss { LEMA_MISS_DENSE = 0, /* v[b, h, 0, :] * 0: a signed zero, NaN f
 const char* lema_last_error(void);
 int lema_abi_version(void);
 
+/* dst[0, bytes) = src[0, bytes) on the device (bytes a multiple of 16, both pointers 16-byte
+ * aligned). No counterpart in the reference: the benchmark's roofline compares the kernels'
+ * HBM rates with this copy's, the streaming rate the memory reaches in practice. */
+int lema_device_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
 /* Sign-pack projected queries or keys into one code per row.
  * Replaces pack_codes, code/lema/attention.py:82-97: bit j of the code of row (b, h, t) is
  * (z[b, h, t, j] >= 0) compared as a float (so -0.0 -> 1, NaN -> 0); LSB = dim 0.

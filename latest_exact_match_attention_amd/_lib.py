@@ -32,6 +32,7 @@ _i64 = ctypes.c_int64
 PROTOTYPES = {
     "lema_last_error": ([], ctypes.c_char_p),
     "lema_abi_version": ([], ctypes.c_int),
+    "lema_device_copy": ([_p, _p, _i64, _p], ctypes.c_int),
     "lema_pack_codes": ([_p, _i32, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _p, _i32, _p],
                         ctypes.c_int),
     "lema_latest_prev_match": ([_p, _p, _i32, _i64, _i64, _p, _i32, _p], ctypes.c_int),

@@ -1,4 +1,5 @@
-// Error reporting and version of liblema_hip.so.
+// Error reporting and version of liblema_hip.so, and the device copy that the benchmark's
+// roofline compares the kernels' HBM rates against.
 #include "lema_internal.h"
 
 namespace lema {
@@ -20,3 +21,52 @@ void clear_error() { g_error[0] = '\0'; }
 extern "C" const char* lema_last_error(void) { return lema::g_error; }
 
 extern "C" int lema_abi_version(void) { return 1; }
+
+namespace lema {
+namespace {
+
+// Each workgroup copies one 32 KB region, its 256 threads 8 16-byte pieces each, 4 in flight,
+// with non-temporal loads and stores. Consecutive workgroups take consecutive regions, so the
+// workgroups resident at any moment work on one compact window of the buffers: on this GPU
+// that reaches 6.2-6.4 TB/s for 1 GiB, against 5.0-5.3 TB/s for a grid-stride loop or for the
+// same regions in a scattered order.
+constexpr int kCopyThreads = 256, kCopyPieces = 2048;
+
+__global__ __launch_bounds__(kCopyThreads) void copy_kernel(const u32x4* __restrict__ src,
+                                                           u32x4* __restrict__ dst, int64_t n16) {
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCopyPieces;
+  for (int i = threadIdx.x; i < kCopyPieces; i += 4 * kCopyThreads) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t at = b0 + i + u * kCopyThreads;
+      if (at < n16) v[u] = __builtin_nontemporal_load(src + at);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t at = b0 + i + u * kCopyThreads;
+      if (at < n16) __builtin_nontemporal_store(v[u], dst + at);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace lema
+
+using namespace lema;
+
+extern "C" int lema_device_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  clear_error();
+  LEMA_REQUIRE(bytes >= 0 && bytes % 16 == 0, "byte count %lld must be a multiple of 16",
+               (long long)bytes);
+  if (bytes == 0) return LEMA_OK;
+  LEMA_REQUIRE(src != nullptr && dst != nullptr && aligned(src, 16) && aligned(dst, 16),
+               "src and dst must be 16-byte aligned device pointers");
+  const int64_t n16 = bytes / 16;
+  const int64_t grid = (n16 + kCopyPieces - 1) / kCopyPieces;
+  LEMA_REQUIRE(grid <= 0x7FFFFFFF, "copy of %lld bytes is too large", (long long)bytes);
+  copy_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kCopyThreads), 0,
+                static_cast<hipStream_t>(stream)>>>(static_cast<const u32x4*>(src),
+                                                    static_cast<u32x4*>(dst), n16);
+  return launch_status("copy_kernel");
+}

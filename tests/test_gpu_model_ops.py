@@ -1,5 +1,6 @@
 """The fused bf16 model segments against the torch ops they replace (plain PyTorch
-references: F.silu(g) * u, nn.RMSNorm after a bf16 add, F.cross_entropy on fp32 logits)."""
+references: F.silu(g) * u, nn.RMSNorm after a bf16 add, F.cross_entropy on fp32 logits), and
+the device copy the benchmark's roofline compares against."""
 import pytest
 import torch
 import torch.nn.functional as F
@@ -88,3 +89,19 @@ def test_embedding_equals_torch(dev):
     bad = torch.tensor([[-1], [50304], [3]], device=dev)
     got = embed(emb, bad)
     assert (got[:2] == 0).all() and torch.equal(got[2], emb.weight[3].view(1, -1))
+
+
+def test_device_copy(dev):
+    """lema_device_copy (the roofline's reference copy) copies every byte, also where the last
+    32 KB region is partial, and refuses sizes that are not whole 16-byte pieces."""
+    from latest_exact_match_attention_amd import _lib
+    st = torch.cuda.current_stream(dev).cuda_stream
+    for n16 in (1, 2047, 2048, 2049, 70001):
+        src = torch.randint(-2**31, 2**31 - 1, (4 * n16,), dtype=torch.int32, device=dev)
+        dst = torch.zeros(4 * n16 + 8, dtype=torch.int32, device=dev)
+        _lib.check(_lib.lib().lema_device_copy(src.data_ptr(), dst.data_ptr(), 16 * n16, st))
+        torch.cuda.synchronize()
+        assert torch.equal(dst[:4 * n16], src), n16
+        assert not dst[4 * n16:].any(), n16           # nothing written past the end
+    with pytest.raises(ValueError):
+        _lib.check(_lib.lib().lema_device_copy(src.data_ptr(), dst.data_ptr(), 24, st))
