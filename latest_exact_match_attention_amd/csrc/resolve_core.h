@@ -78,7 +78,12 @@ __device__ __forceinline__ uint32_t filter_hash(uint32_t h) { return (h * 0x2C1B
 constexpr int kWideBits = 32768;
 constexpr int kQueueCap = 384;
 constexpr int kScanGroup = 4;  // key batches whose loads the queued scan issues together
-__device__ __forceinline__ uint32_t wide_hash(uint32_t h) { return (h * 0x9E3779B1u) >> 17; }
+// The scan tests every earlier key with it, so it avoids the quarter-rate 32-bit multiply:
+// the high half is folded into the low 24 bits, which a full-rate 24-bit multiply mixes.
+// (__umul24 is declared to return int: the product is shifted as unsigned.)
+__device__ __forceinline__ uint32_t wide_hash(uint32_t h) {
+  return static_cast<uint32_t>(__umul24((h ^ (h >> 16)) & 0xFFFFFFu, 0x9E3779u)) >> 17;
+}
 
 template <typename CodeT>
 struct ResolveLds {
