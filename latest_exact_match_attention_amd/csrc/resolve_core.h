@@ -64,7 +64,8 @@ static_assert(kChunk / 64 <= 16, "word summary is a 16-bit mask");
 // seldom repeat (pre-activation codes of a language model) then cost one 4-byte LDS read
 // each. LEMA_RESOLVE_FILTER: 0 never, 1 always, 2 in chunks of more than kFilterMinCodes
 // distinct query codes (on Zipf-distributed codes, ~370 per chunk, the filter passes most
-// keys and only adds a read).
+// keys and only adds a read). Chunks that scan through the wider filter below (no chunk
+// summaries) use that one for their own keys too and do not build this one.
 #ifndef LEMA_RESOLVE_FILTER
 #define LEMA_RESOLVE_FILTER 2
 #endif
