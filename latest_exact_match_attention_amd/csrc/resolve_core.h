@@ -738,9 +738,10 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       }
       flush();
       // Does some key of the chunk carry a query code of the chunk? Codes that seldom repeat
-      // usually give none (C5's layers: ~97% of chunks), and then no query has an in-chunk
-      // match: every answer is the code's latest position before the chunk, and the map, the
-      // chunk's own keys and the per-query map lookups are skipped.
+      // usually give none (a 64-head language model's 24-bit codes at 16K tokens: 90-97% of
+      // chunks), and then no query has an in-chunk match: every answer is the code's latest
+      // position before the chunk, and the map, the chunk's own keys and the per-query map
+      // lookups are skipped.
       int sl[kPer];
       find_codes(kk, sl);
       bool hit = false;
