@@ -122,12 +122,18 @@ __device__ __forceinline__ void read_bucket(const CodeT* base, int b, CodeT (&x)
   }
 }
 
-// Slot of `key` among the bucket's 4 (first match), or -1; `open` gets whether an empty slot
-// was seen, which ends a probe sequence.
+// The filled slots of a bucket are always a prefix of its 4: an insert claims the first free
+// slot it saw, slots are never freed, and a claim that loses its slot reads the bucket again.
+// So a bucket whose last slot is free has room (a probe sequence ends there), and its first
+// free slot is the number of filled ones. A key is in at most one slot.
+// Slot of `key` among the bucket's 4, or -1, without branches; `open` gets whether the bucket
+// has room.
 template <typename KeyT>
 __device__ __forceinline__ int match4(const KeyT (&x)[4], KeyT key, KeyT empty, bool& open) {
-  open = x[0] == empty || x[1] == empty || x[2] == empty || x[3] == empty;
-  return x[0] == key ? 0 : x[1] == key ? 1 : x[2] == key ? 2 : x[3] == key ? 3 : -1;
+  open = x[3] == empty;
+  const bool m1 = x[1] == key, m2 = x[2] == key, m3 = x[3] == key;
+  const int e = (m1 ? 1 : 0) | (m2 ? 2 : 0) | (m3 ? 3 : 0);
+  return x[0] == key || m1 || m2 || m3 ? e : -1;
 }
 
 // Insert `key` into a table of NB buckets (or find it): returns its slot; `inserted` tells
@@ -150,7 +156,7 @@ __device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int
       b = b + 1 == NB ? 0 : b + 1;
       continue;
     }
-    const int f = x[0] == empty ? 0 : x[1] == empty ? 1 : x[2] == empty ? 2 : 3;
+    const int f = (x[0] != empty ? 1 : 0) + (x[1] != empty ? 1 : 0) + (x[2] != empty ? 1 : 0);
     const KeyT old = lds_cas(&base[4 * b + f], empty, key);
     if (old == empty) inserted = true;
     if (old == empty || old == key) return 4 * b + f;
@@ -465,21 +471,6 @@ __device__ __forceinline__ void gather_rows(const GatherArgs& g, int64_t row, in
     gather_rows_as<VEC, kInFlight, kInFlightP2, false>(g, row, c0, nrows, t, nthreads, src_of);
 }
 
-// Find 4 keys at once (first bucket reads issued together); -1 where absent or inactive.
-template <typename KeyT, int NB>
-__device__ __forceinline__ void find4(const KeyT* base, const KeyT (&key)[4], KeyT empty,
-                                      int (&slot)[4]) {
-  int b[4];
-  KeyT x[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    b[i] = bucket_of<NB>(fold(key[i]));
-    read_bucket(base, b[i], x[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) slot[i] = table_find<KeyT, NB>(base, key[i], empty, b[i], x[i]);
-}
-
 // find4 for the keys with pass[i] set (the others get -1 without touching the table).
 template <typename KeyT, int NB>
 __device__ __forceinline__ void find4_masked(const KeyT* base, const KeyT (&key)[4], KeyT empty,
@@ -491,9 +482,35 @@ __device__ __forceinline__ void find4_masked(const KeyT* base, const KeyT (&key)
     b[i] = bucket_of<NB>(fold(key[i]));
     if (pass[i]) read_bucket(base, b[i], x[i]);
   }
+  // The first bucket answers almost every lookup: matched without branches; a full bucket
+  // without the key sends the wavefront on to the next buckets (rarely).
+  bool more[4];
+  bool any = false;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    slot[i] = pass[i] ? table_find<KeyT, NB>(base, key[i], empty, b[i], x[i]) : -1;
+  for (int i = 0; i < 4; ++i) {
+    bool open;
+    const int e = match4(x[i], key[i], empty, open);
+    slot[i] = pass[i] && e >= 0 ? 4 * b[i] + e : -1;
+    more[i] = pass[i] && e < 0 && !open;
+    any = any || more[i];
+  }
+  if (__ballot(any) != 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!more[i]) continue;
+      const int nb = b[i] + 1 == NB ? 0 : b[i] + 1;
+      read_bucket(base, nb, x[i]);
+      slot[i] = table_find<KeyT, NB>(base, key[i], empty, nb, x[i]);
+    }
+  }
+}
+
+// Find 4 keys at once (first bucket reads issued together); -1 where absent or inactive.
+template <typename KeyT, int NB>
+__device__ __forceinline__ void find4(const KeyT* base, const KeyT (&key)[4], KeyT empty,
+                                      int (&slot)[4]) {
+  const bool all[4] = {true, true, true, true};
+  find4_masked<KeyT, NB>(base, key, empty, all, slot);
 }
 
 // Resolve the 1024 queries of chunk `chunk` of row `row` with the 256 threads t = 0..255
@@ -780,9 +797,12 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
           if (j0 - kPrefetch * kBatch >= 0) load_batch(nxt[d], j0 - kPrefetch * kBatch);
           int sl[4];
           find_codes(cur, sl);
-          int32_t known[4];  // read only for keys of query codes (the others raise nothing)
+          int32_t known[4];  // read for every key (slot kSlots stands in for the others, which
+                             // raise nothing), so the reads need no branches
 #pragma unroll
-          for (int e = 0; e < 4; ++e) known[e] = sl[e] >= 0 ? s.pos[sl[e]] : 0x7FFFFFFF;
+          for (int e = 0; e < 4; ++e) known[e] = s.pos[sl[e] >= 0 ? sl[e] : kSlots];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) known[e] = sl[e] >= 0 ? known[e] : 0x7FFFFFFF;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int32_t j = key_pos(j0, e);
