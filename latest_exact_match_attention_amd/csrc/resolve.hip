@@ -238,9 +238,6 @@ int fill_gather(GatherArgs& g, const void* v, int32_t dtype, int64_t H, int64_t 
   g.y_st = y_st * es;
   g.pieces = static_cast<uint32_t>(rb / vec);
   g.pdiv = FastDiv(g.pieces);
-  g.plog = -1;
-  for (int l = 0; l <= 6; ++l)
-    if (g.pieces == (1u << l)) g.plog = l;
   g.miss = miss;
   g.dtype = dtype;
   g.nt = y_st == dv;  // rows of y adjacent: stream them out; else let L2 merge the pieces

@@ -188,7 +188,6 @@ struct GatherArgs {
   int64_t y_sb, y_sh, y_st;
   uint32_t pieces;  // 16/8/4/2-byte pieces per value row
   FastDiv pdiv;     // division by `pieces`
-  int32_t plog;     // log2(pieces) when pieces is a power of two <= 64, else -1
   int32_t miss;
   int32_t dtype;
   int32_t nt;  // non-temporal stores of y (rows of y adjacent); plain stores let L2 merge the
@@ -382,9 +381,15 @@ struct Piece<2> {
 };
 
 // Copy the value rows of `nrows` consecutive positions starting at c0 of row (b, h): y[c0 + r]
-// = v[src_of(r)]. Thread `t` of `nthreads` takes pieces t, t + nthreads, ..., with kInFlight
-// independent loads issued before the first store. An index outside [0, T) is filled like a
-// miss, so no index can make the kernel read outside v.
+// = v[src_of(r)]. An index outside [0, T) is filled like a miss, so no index can make the
+// kernel read outside v.
+// Rows of at most nthreads pieces: thread t always copies piece t % pieces of rows
+// t / pieces + k * (nthreads / pieces) (consecutive threads on consecutive pieces of
+// consecutive rows), so its miss value (from v's first row, or zero) is formed once, and each
+// piece is one conditional load and one store, kInFlightP2 loads issued before the first
+// store. (A miss must not load into the same registers as a copy: the two loads would then be
+// waited for one by one.) Longer rows: thread t takes pieces t, t + nthreads, ..., with
+// kInFlight independent loads issued before the first store.
 template <int VEC, int kInFlight, int kInFlightP2, bool NT, typename SrcFn>
 __device__ __forceinline__ void gather_rows_as(const GatherArgs& g, int64_t row, int64_t c0,
                                                int nrows, int t, int nthreads, SrcFn src_of) {
@@ -392,36 +397,35 @@ __device__ __forceinline__ void gather_rows_as(const GatherArgs& g, int64_t row,
   const int64_t b = row / g.H, h = row - (row / g.H) * g.H;
   const uint8_t* vbase = g.v + b * g.v_sb + h * g.v_sh;
   uint8_t* ybase = g.y + b * g.y_sb + h * g.y_sh + c0 * g.y_st;
-  if (g.plog >= 0) {
-    // pieces = 2^plog divides the block: thread t always copies piece t % pieces of rows
-    // t / pieces + k * (nthreads / pieces), with kInFlight of them loaded before storing
-    const int rpp = nthreads >> g.plog;
-    const int r0 = t >> g.plog, pc = t & ((1 << g.plog) - 1);
+  if (g.pieces <= static_cast<uint32_t>(nthreads)) {
+    const int pieces = static_cast<int>(g.pieces);
+    const int rpp = static_cast<int>(g.pdiv.div(static_cast<uint32_t>(nthreads)));
+    const int r0 = static_cast<int>(g.pdiv.div(static_cast<uint32_t>(t)));
+    if (r0 >= rpp) return;  // the threads past rpp * pieces
+    const int pc = t - r0 * pieces;
     const uint8_t* vp = vbase + pc * VEC;
     uint8_t* yp = ybase + pc * VEC;
+    const typename P::T missv = g.miss == LEMA_MISS_ZERO ? P::zero() : P::miss(P::load(vp), g.dtype);
     for (int rb = r0; rb < nrows; rb += kInFlightP2 * rpp) {
       typename P::T val[kInFlightP2];
-      int32_t sv[kInFlightP2];
+      int32_t sv[kInFlightP2];  // source position, -1 a miss, -2 past the chunk's rows
+      int64_t x[kInFlightP2];  // read for every u (a row inside the chunk stands in), so
+                               // the reads are issued together
 #pragma unroll
       for (int u = 0; u < kInFlightP2; ++u) {
         const int r = rb + u * rpp;
-        const int64_t x = r < nrows ? src_of(r) : -2;
-        sv[u] = r >= nrows ? -2 : (x >= 0 && x < g.T ? static_cast<int32_t>(x) : -1);
+        x[u] = src_of(r < nrows ? r : nrows - 1);
       }
 #pragma unroll
-      for (int u = 0; u < kInFlightP2; ++u) {
-        if (sv[u] >= 0)
-          val[u] = P::load(vp + sv[u] * g.v_st);
-        else if (sv[u] == -1 && g.miss != LEMA_MISS_ZERO)
-          val[u] = P::load(vp);
-      }
+      for (int u = 0; u < kInFlightP2; ++u)
+        sv[u] = rb + u * rpp >= nrows ? -2 : (x[u] >= 0 && x[u] < g.T ? static_cast<int32_t>(x[u]) : -1);
 #pragma unroll
-      for (int u = 0; u < kInFlightP2; ++u) {
-        if (sv[u] == -2) continue;
-        const typename P::T out = sv[u] >= 0 ? val[u]
-                                  : (g.miss == LEMA_MISS_ZERO ? P::zero() : P::miss(val[u], g.dtype));
-        P::template store<NT>(yp + static_cast<int64_t>(rb + u * rpp) * g.y_st, out);
-      }
+      for (int u = 0; u < kInFlightP2; ++u)
+        if (sv[u] >= 0) val[u] = P::load(vp + static_cast<int64_t>(sv[u]) * g.v_st);
+#pragma unroll
+      for (int u = 0; u < kInFlightP2; ++u)
+        if (sv[u] != -2)
+          P::template store<NT>(yp + static_cast<int64_t>(rb + u * rpp) * g.y_st, sv[u] >= 0 ? val[u] : missv);
     }
     return;
   }
