@@ -136,12 +136,12 @@ __device__ __forceinline__ int match4(const KeyT (&x)[4], KeyT key, KeyT empty, 
   return x[0] == key || m1 || m2 || m3 ? e : -1;
 }
 
-// Insert `key` into a table of NB buckets (or find it): returns its slot; `inserted` tells
-// whether this call put it there. The table must have an empty slot somewhere (load < 1
-// here). Torn 8-byte reads are re-checked atomically.
+// Insert `key` into a table of NB buckets (or find it), probing from bucket b: returns its
+// slot; `inserted` tells whether this call put it there. The table must have an empty slot
+// somewhere (load < 1 here). Torn 8-byte reads are re-checked atomically.
 template <typename KeyT, int NB>
-__device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int b,
-                                           bool& inserted) {
+__device__ __forceinline__ int table_claim_loop(KeyT* base, KeyT key, KeyT empty, int b,
+                                                bool& inserted) {
   inserted = false;
   for (;;) {
     KeyT x[4];
@@ -162,6 +162,31 @@ __device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int
     if (old == empty || old == key) return 4 * b + f;
     // another key took that slot first: read the same bucket again
   }
+}
+
+// table_claim_loop with its first round written out: one bucket read, then either the key's
+// slot or one CAS at the bucket's first free slot, without the loop's branches. Lanes that
+// meet a full bucket, a lost CAS or (8-byte keys) a torn read go on in the loop, behind a
+// branch that is uniform across the lanes taking part.
+template <typename KeyT, int NB>
+__device__ __forceinline__ int table_claim(KeyT* base, KeyT key, KeyT empty, int b,
+                                           bool& inserted) {
+  KeyT x[4];
+  read_bucket(base, b, x);
+  bool open;
+  const int e = match4(x, key, empty, open);
+  const int f = (x[0] != empty ? 1 : 0) + (x[1] != empty ? 1 : 0) + (x[2] != empty ? 1 : 0);
+  int slot = -1;
+  inserted = false;
+  if (e >= 0) {
+    if (sizeof(KeyT) == 4 || lds_cas(&base[4 * b + e], key, key) == key) slot = 4 * b + e;
+  } else if (open) {
+    const KeyT old = lds_cas(&base[4 * b + f], empty, key);
+    inserted = old == empty;
+    if (old == empty || old == key) slot = 4 * b + f;
+  }
+  if (__ballot(slot < 0) != 0 && slot < 0) slot = table_claim_loop<KeyT, NB>(base, key, empty, b, inserted);
+  return slot;
 }
 
 // Finish a lookup whose first bucket b was read into x: slot of key, or -1 (no concurrent
