@@ -201,6 +201,45 @@ def test_gather_golden(dev, dtype, miss):
     assert torch.equal(y32.view(torch.uint8), y.view(torch.uint8))
 
 
+@pytest.mark.parametrize("dv,dtype", [(1, "bf16"), (3, "bf16"), (5, "f32"), (40, "bf16"),
+                                      (100, "f32"), (1100, "f32"), (2100, "bf16")])
+def test_value_row_shapes(dev, dv, dtype):
+    """Value rows of 2 B to 4.4 KB through the fused path and the standalone gather: pieces of
+    2, 4, 8 and 16 bytes, piece counts that leave threads of the workgroup idle (3, 5, 25),
+    and rows of more than 256 pieces (275 and 525: the strided copy). Row 0 holds -0, NaN and
+    -inf, the dense miss fill's source."""
+    B, H, T = 1, 3, 1500
+    rng = np.random.default_rng(dv)
+    qc = rng.integers(0, 1000, size=(B, H, T)).astype(np.int32)
+    kc = rng.integers(0, 1000, size=(B, H, T)).astype(np.int32)
+    v32 = rng.standard_normal((B, H, T, dv)).astype(np.float32)
+    v32[:, :, 0, 0] = -0.0
+    if dv > 1:
+        v32[:, :, 0, 1] = np.nan
+    if dv > 2:
+        v32[:, :, 0, 2] = -np.inf
+    v = torch.from_numpy(v32).to(dev)
+    if dtype == "bf16":
+        v = v.to(torch.bfloat16)
+
+    def carrier(t):
+        t = t.contiguous().cpu()
+        return t.numpy() if dtype == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+    q, k = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+    y, src = lema_from_codes(q, k, v, return_src=True)
+    want_src = oracle.latest_prev_match(qc.reshape(B * H, T), kc.reshape(B * H, T))
+    assert np.array_equal(src.cpu().numpy().reshape(B * H, T), want_src)
+    vc = carrier(v).reshape(B * H, T, dv)
+    want = oracle.gather(vc, dtype, want_src, 0)
+    assert same_values(carrier(y).reshape(want.shape), want, dtype)
+    assert 0.2 < (want_src < 0).mean() < 0.8  # both copies and misses
+    for miss, mode in (("dense", 0), ("zero", 1)):
+        yg = gather_values(v, src, miss=miss)
+        want = oracle.gather(vc, dtype, want_src, mode)
+        assert same_values(carrier(yg).reshape(want.shape), want, dtype), miss
+
+
 def test_dense_plumbing_workload(dev):
     """B1 H8 T4096, 16-bit codes, fp32 values: indices and outputs bit-exact."""
     qc, kc, v = dense_plumbing(0)
