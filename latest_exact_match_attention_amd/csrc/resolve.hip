@@ -31,6 +31,8 @@
 // of each source row and the (non-temporal) writes of y are coalesced.
 #include "resolve_core.h"
 
+#include <atomic>
+
 #ifndef LEMA_GATHER_INFLIGHT
 #define LEMA_GATHER_INFLIGHT 12  // value pieces in flight per thread (pieces a power of two)
 #endif
@@ -38,22 +40,17 @@
 namespace lema {
 namespace {
 
-// One workgroup (256 threads) per (row, chunk): resolve, then (VEC > 0) gather the chunk's
-// value rows. XCD-aware work mapping: workgroup b runs on XCD b % 8. When the rows come in
-// whole groups of 64, rows 8g..8g+7 belong to XCD g % 8 and its workgroups take one chunk of
-// all 8 rows back to back, latest chunks first: the 8 rows' key codes and value rows share
-// that XCD's L2, and where y interleaves the rows (y viewed from [B, T, H * dv]) their pieces
-// of each output line are written close together in the same L2 (measured: 116 -> 112 us on
-// B8 H16 T16384 Zipf codes; 307 -> 172 us, with the filter, on a language-model layer of B4
-// H64 T16384 d 24). Otherwise every chunk of row r runs on XCD r % 8, latest chunks first.
-template <typename CodeT, int VEC, bool kSumm>
-__global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
-  __shared__ ResolveLds<CodeT> s;
-  const int bid = blockIdx.x;
-  const int xcd = bid % kNumXcd;
-  const int k = bid / kNumXcd;
-  int chunk;
-  int64_t row;
+// Work item v of the resolver's grid is one (row, chunk). XCD-aware order: item v runs on
+// XCD v % 8. When the rows come in whole groups of 64, rows 8g..8g+7 belong to XCD g % 8 and
+// its items take one chunk of all 8 rows back to back, latest chunks first: the 8 rows' key
+// codes and value rows share that XCD's L2, and where y interleaves the rows (y viewed from
+// [B, T, H * dv]) their pieces of each output line are written close together in the same L2
+// (measured: 116 -> 112 us on B8 H16 T16384 Zipf codes; 307 -> 172 us, with the filter, on a
+// language-model layer of B4 H64 T16384 d 24). Otherwise every chunk of row r runs on XCD
+// r % 8, latest chunks first.
+__device__ __forceinline__ void item_of(const ResolveArgs& a, int v, int64_t& row, int& chunk) {
+  const int xcd = v % kNumXcd;
+  const int k = v / kNumXcd;
   if (a.group) {
     const int per = kNumXcd * a.nchunks;
     chunk = a.nchunks - 1 - (k % per) / kNumXcd;
@@ -62,6 +59,16 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
     chunk = a.nchunks - 1 - (k % a.nchunks);
     row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
   }
+}
+
+// One workgroup (256 threads) per work item: resolve the chunk, then (VEC > 0) copy its value
+// rows.
+template <typename CodeT, int VEC, bool kSumm>
+__global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
+  __shared__ ResolveLds<CodeT> s;
+  int64_t row;
+  int chunk;
+  item_of(a, blockIdx.x, row, chunk);
   if (row >= a.N) return;
   const int t = threadIdx.x;
   int32_t src[kPer];
@@ -76,7 +83,75 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
     const int32_t c0 = chunk * kChunk;
     const int n_here = static_cast<int>(a.T - c0 < kChunk ? a.T - c0 : kChunk);
     gather_rows<VEC, 8, LEMA_GATHER_INFLIGHT>(a.g, row, c0, n_here, t, kThreads,
-                            [&](uint32_t r) -> int64_t { return srcs[r]; });
+                                              [&](uint32_t r) -> int64_t { return srcs[r]; });
+  }
+}
+
+// Persistent form of resolve_kernel with copies. As many workgroups as the GPU holds at once
+// take work items blockIdx.x, + gridDim.x, ... (gridDim.x a multiple of 8 keeps every item on
+// its XCD). The workgroups of every other block of 128 copy each chunk one item late: they
+// resolve the next chunk first, holding the previous chunk's indices in four registers per
+// thread. Launched all at once, workgroups that each resolve and then copy stay in step,
+// round after round: the whole chip resolves (HBM idle), and then it copies. With half of
+// them a chunk behind, resolving and copying run side by side. Measured on B8 H16 T16384 Zipf
+// codes (d_v 64): 84.3 us with one workgroup per item, 77.5 us this way; on a language-model
+// layer (B4 H64 T16384, d_v 24): 104.1 and 91.0 us.
+template <typename CodeT, int VEC, bool kSumm>
+__global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_lag_kernel(ResolveArgs a, int32_t items) {
+  static_assert(VEC > 0, "the persistent form exists for copies");
+  __shared__ ResolveLds<CodeT> s;
+  const int bid = blockIdx.x, G = gridDim.x;
+  const bool lagged = (bid >> 7) & 1;
+  auto bar = [] { __syncthreads(); };
+  int32_t* srcs = reinterpret_cast<int32_t*>(s.mbits);  // the masks are dead while copying
+  const int n = bid < items ? (items - bid + G - 1) / G : 0;
+  int32_t keep[kPer] = {-1, -1, -1, -1};  // the lagged chunk's indices
+  int64_t krow = a.N;
+  int kch = 0;
+#pragma unroll 1
+  for (int i = 0; i < n + (lagged ? 1 : 0); ++i) {
+    // The thread index through an opaque copy: what the resolver derives from it is formed
+    // in each iteration instead of being hoisted out of the loop and held in registers
+    // across all of it (4 workgroups per CU leave 128 VGPRs).
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    int64_t row = a.N;
+    int chunk = 0;
+    if (i < n) item_of(a, bid + i * G, row, chunk);
+    int32_t src[kPer] = {-1, -1, -1, -1};
+    const bool resolved = row < a.N;
+    if (resolved) {
+      resolve_chunk<CodeT, decltype(bar), kSumm>(s, a, row, chunk, t, bar, src);
+      bar();  // every wavefront's last table read, before the masks' storage takes indices
+    }
+    {
+      int64_t crow = row;
+      int cchunk = chunk;
+      int32_t c[kPer];
+#pragma unroll
+      for (int p = 0; p < kPer; ++p) c[p] = src[p];
+      if (lagged) {
+        crow = krow;
+        cchunk = kch;
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+          c[p] = keep[p];
+          keep[p] = src[p];
+        }
+        krow = resolved ? row : a.N;
+        kch = chunk;
+      }
+      if (crow < a.N) {
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) srcs[p * kThreads + t] = c[p];
+        bar();
+        const int32_t c0 = cchunk * kChunk;
+        const int n_here = static_cast<int>(a.T - c0 < kChunk ? a.T - c0 : kChunk);
+        gather_rows<VEC, 8, LEMA_GATHER_INFLIGHT>(a.g, crow, c0, n_here, t, kThreads,
+                                                  [&](uint32_t r) -> int64_t { return srcs[r]; });
+        bar();  // the copy's last index read, before the next chunk's tables start over
+      }
+    }
   }
 }
 
@@ -265,17 +340,63 @@ int launch_resolve(ResolveArgs& a, int vec, hipStream_t st) {
   return launch_vec<CodeT, false>(a, vec, grid, st);
 }
 
+// Workgroups of `kernel` (256 threads) the current GPU holds at once, 0 if unknown; kept in
+// `per_dev` (one array per kernel: every instantiation of a kernel template has the same
+// function type) after the first call on a device.
+constexpr int kMaxDev = 64;
+template <typename K>
+int64_t resident_groups(K kernel, std::atomic<int> (&per_dev)[kMaxDev]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  int n = per_dev[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess)
+      return 0;
+    n = cus * per_cu;
+    per_dev[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// `items` work items. With copies, and more items than the GPU holds workgroups at once,
+// resolve_lag_kernel gives each workgroup k = ceil(items / resident) of them (some k - 1),
+// from a grid that is a multiple of 8, when that grid keeps at least 90% of the resident
+// slots busy. Otherwise resolve_kernel runs one workgroup per item. Items that do not spread
+// evenly would leave some workgroups an extra chunk at the end; with one workgroup per item
+// the dispatcher fills the slots as they free up (measured striped: 1152 items on 1024 slots
+// 45.8 against 38.6 us one per item; 2048 items of 8-byte codes on 768 slots, 89.0 against
+// 75.1 us).
+template <typename CodeT, int VEC, bool kSumm>
+int launch_items(ResolveArgs& a, int64_t items, hipStream_t st) {
+  if constexpr (VEC > 0) {
+    const auto lag = resolve_lag_kernel<CodeT, VEC, kSumm>;
+    static std::atomic<int> per_dev[kMaxDev];
+    const int64_t resident = resident_groups(lag, per_dev) / kNumXcd * kNumXcd;
+    if (resident >= kNumXcd && items > resident) {
+      const int64_t k = (items + resident - 1) / resident;
+      const int64_t g = ((items + k - 1) / k + kNumXcd - 1) / kNumXcd * kNumXcd;
+      if (10 * g >= 9 * resident) {
+        lag<<<dim3(g), dim3(kThreads), 0, st>>>(a, static_cast<int32_t>(items));
+        return launch_status("resolve_lag_kernel");
+      }
+    }
+  }
+  resolve_kernel<CodeT, VEC, kSumm><<<dim3(items), dim3(kThreads), 0, st>>>(a);
+  return launch_status("resolve_kernel");
+}
+
 template <typename CodeT, bool kSumm>
 int launch_vec(ResolveArgs& a, int vec, int64_t grid, hipStream_t st) {
   switch (vec) {
-    case 0: resolve_kernel<CodeT, 0, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 16: resolve_kernel<CodeT, 16, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 8: resolve_kernel<CodeT, 8, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 4: resolve_kernel<CodeT, 4, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
-    case 2: resolve_kernel<CodeT, 2, kSumm><<<dim3(grid), dim3(kThreads), 0, st>>>(a); break;
+    case 0: return launch_items<CodeT, 0, kSumm>(a, grid, st);
+    case 16: return launch_items<CodeT, 16, kSumm>(a, grid, st);
+    case 8: return launch_items<CodeT, 8, kSumm>(a, grid, st);
+    case 4: return launch_items<CodeT, 4, kSumm>(a, grid, st);
+    case 2: return launch_items<CodeT, 2, kSumm>(a, grid, st);
     default: set_error("internal: piece size %d", vec); return LEMA_BAD_ARG;
   }
-  return launch_status("resolve_kernel");
 }
 
 int check_rows(const void* qc, const void* kc, int32_t code_bytes, int64_t N, int64_t T) {

@@ -240,6 +240,33 @@ def test_value_row_shapes(dev, dv, dtype):
         assert same_values(carrier(yg).reshape(want.shape), want, dtype), miss
 
 
+@pytest.mark.parametrize("N,T,code_dtype,dv", [
+    (72, 27000, torch.int32, 24),    # 1944 items on 976 workgroups: some take 2, some 1
+    (64, 29500, torch.int32, 64),    # grouped order, a partial last chunk
+    (128, 12000, torch.int64, 32),   # 8-byte codes: 3 workgroups per CU
+    (16, 131072, torch.int32, 8),    # 128 chunks per row: the chunk summaries
+])
+def test_persistent_copy_shapes(dev, N, T, code_dtype, dv):
+    """Shapes with more chunks than the GPU holds workgroups at once, where one workgroup
+    resolves and copies several chunks (half of them copying each chunk one item late):
+    indices and values against the oracle."""
+    rng = np.random.default_rng(N + T)
+    alpha = T // 2  # about 43% misses
+    qc = rng.integers(0, alpha, size=(1, N, T))
+    kc = rng.integers(0, alpha, size=(1, N, T))
+    v = torch.from_numpy(rng.standard_normal((1, N, T, dv)).astype(np.float32)).to(dev)
+    v = v.to(torch.bfloat16)
+    q = torch.from_numpy(qc).to(dev).to(code_dtype)
+    k = torch.from_numpy(kc).to(dev).to(code_dtype)
+    y, src = lema_from_codes(q, k, v, return_src=True)
+    want_src = oracle.latest_prev_match(qc.reshape(N, T), kc.reshape(N, T))
+    assert np.array_equal(src.cpu().numpy().reshape(N, T), want_src)
+    vc = bits16(v).reshape(N, T, dv)
+    want = oracle.gather(vc, "bf16", want_src, 0)
+    assert same_values(bits16(y).reshape(want.shape), want, "bf16")
+    assert 0.05 < (want_src < 0).mean() < 0.95
+
+
 def test_dense_plumbing_workload(dev):
     """B1 H8 T4096, 16-bit codes, fp32 values: indices and outputs bit-exact."""
     qc, kc, v = dense_plumbing(0)
