@@ -244,8 +244,8 @@ def bench_prefill(a):
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("resolve_kernel/zipf_prefill"),
-                     "kernel": "resolve_kernel (fused resolve + gather)",
+                     "traffic": load_traffic("resolve_lag_kernel/zipf_prefill"),
+                     "kernel": "resolve_lag_kernel (fused resolve + gather, persistent)",
                      "bytes_per_query": BYTES_PER_QUERY, "queries_per_launch": nq,
                      "copy_measured": {"GBps": copy_gbps, "frac": achieved / copy_gbps,
                                        "what": "lema_device_copy of the value tensor (read + "
@@ -604,7 +604,7 @@ def bench_lm(a):
                      "unit": "TFLOP/s", "frac": tflops / MFMA_BF16_PEAK_TFLOPS,
                      "traffic": None, "kernel": "whole forward (GEMM FLOPs / step time)",
                      "flops_per_token": lm_flops_per_token(cfg)},
-        "lema_kernel": {"kernel": "resolve_kernel (fused resolve + gather), one layer",
+        "lema_kernel": {"kernel": "resolve_lag_kernel (fused resolve + gather), one layer",
                         "us": ms_l * 1e3, "queries": nq, "bytes_per_query": bpq,
                         "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS},
         "pack_kernel": {"kernel": "pack_dense_kernel, one layer's query codes",
