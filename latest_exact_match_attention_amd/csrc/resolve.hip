@@ -48,17 +48,20 @@ namespace {
 // (measured: 116 -> 112 us on B8 H16 T16384 Zipf codes; 307 -> 172 us, with the filter, on a
 // language-model layer of B4 H64 T16384 d 24). Otherwise every chunk of row r runs on XCD
 // r % 8, latest chunks first.
-__device__ __forceinline__ void item_of(const ResolveArgs& a, int v, int64_t& row, int& chunk) {
+__device__ __forceinline__ void item_rc(int nchunks, bool group, int v, int64_t& row, int& chunk) {
   const int xcd = v % kNumXcd;
   const int k = v / kNumXcd;
-  if (a.group) {
-    const int per = kNumXcd * a.nchunks;
-    chunk = a.nchunks - 1 - (k % per) / kNumXcd;
+  if (group) {
+    const int per = kNumXcd * nchunks;
+    chunk = nchunks - 1 - (k % per) / kNumXcd;
     row = (static_cast<int64_t>(k / per) * kNumXcd + xcd) * kNumXcd + (k % per) % kNumXcd;
   } else {
-    chunk = a.nchunks - 1 - (k % a.nchunks);
-    row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
+    chunk = nchunks - 1 - (k % nchunks);
+    row = static_cast<int64_t>(k / nchunks) * kNumXcd + xcd;
   }
+}
+__device__ __forceinline__ void item_of(const ResolveArgs& a, int v, int64_t& row, int& chunk) {
+  item_rc(a.nchunks, a.group != 0, v, row, chunk);
 }
 
 // One workgroup (256 threads) per work item: resolve the chunk, then (VEC > 0) copy its value
@@ -254,17 +257,20 @@ struct GatherOnlyArgs {
   int32_t src_bytes;
   int64_t N, T;
   int32_t nchunks;
+  int32_t group;  // the resolver's grouped order (8 rows of one XCD take a chunk together)
   GatherArgs g;
 };
 
+// One workgroup per (row, 1024 positions), in the resolver's order: where y interleaves the
+// rows (viewed from [B, T, H * dv]), the 8 rows of one XCD write whole output lines together
+// in its L2. (Rows spread over the XCDs wrote each line in parts from several L2s: a
+// language-model layer's output, B4 H64 T16384 d_v 24, took 82.5 us that way.)
 template <int VEC>
 __global__ __launch_bounds__(256) void gather_kernel(GatherOnlyArgs a) {
   __shared__ int32_t ssrc[kGatherRows];
-  const int bid = blockIdx.x;
-  const int xcd = bid % kNumXcd;
-  const int k = bid / kNumXcd;
-  const int chunk = k % a.nchunks;
-  const int64_t row = static_cast<int64_t>(k / a.nchunks) * kNumXcd + xcd;
+  int64_t row;
+  int chunk;
+  item_rc(a.nchunks, a.group != 0, blockIdx.x, row, chunk);
   if (row >= a.N) return;
   const int64_t c0 = static_cast<int64_t>(chunk) * kGatherRows;
   const int nrows = static_cast<int>(a.T - c0 < kGatherRows ? a.T - c0 : kGatherRows);
@@ -541,7 +547,10 @@ extern "C" int lema_gather(const void* v, int32_t dtype, int64_t B, int64_t H, i
   a.N = N;
   a.T = T;
   a.nchunks = static_cast<int32_t>((T + kGatherRows - 1) / kGatherRows);
-  const int64_t grid = (N + kNumXcd - 1) / kNumXcd * kNumXcd * a.nchunks;
+  a.group = N % 64 == 0;
+  const int64_t groups = (N + kNumXcd - 1) / kNumXcd;
+  const int64_t grid = a.group ? (groups + kNumXcd - 1) / kNumXcd * kNumXcd * kNumXcd * a.nchunks
+                               : (N + kNumXcd - 1) / kNumXcd * kNumXcd * a.nchunks;
   LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows x chunks");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (vec) {
