@@ -267,6 +267,35 @@ def test_persistent_copy_shapes(dev, N, T, code_dtype, dv):
     assert 0.05 < (want_src < 0).mean() < 0.95
 
 
+def test_persistent_copy_in_a_graph(dev):
+    """The fused op captured in a HIP graph on a shape that takes the persistent kernel (1944
+    items): every replay, with eager work between them, equals the eager result."""
+    N, T, dv = 72, 27000, 24
+    rng = np.random.default_rng(5)
+    q = torch.from_numpy(rng.integers(0, T // 2, size=(1, N, T))).to(dev).to(torch.int32)
+    k = torch.from_numpy(rng.integers(0, T // 2, size=(1, N, T))).to(dev).to(torch.int32)
+    v = torch.randn(1, N, T, dv, device=dev).to(torch.bfloat16)
+    want, want_src = lema_from_codes(q, k, v, return_src=True)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm-up on the capturing stream
+        lema_from_codes(q, k, v, return_src=True)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y, src = lema_from_codes(q, k, v, return_src=True)
+    for rep in range(3):
+        y.zero_()
+        src.fill_(-7)
+        noise = torch.randn(1 << 20, device=dev).sum()  # eager work between the replays
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.isfinite(noise)
+        assert torch.equal(src, want_src), rep
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16)), rep
+
+
 def test_dense_plumbing_workload(dev):
     """B1 H8 T4096, 16-bit codes, fp32 values: indices and outputs bit-exact."""
     qc, kc, v = dense_plumbing(0)
