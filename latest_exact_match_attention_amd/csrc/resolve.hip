@@ -18,8 +18,9 @@
 // no scratch memory. Step (c) costs O(T^2 / 1024) lookups per row, reading the row's key
 // codes from L2 with 16-byte loads one batch ahead; at T = 16k that is 7.5 per query.
 //
-// With a workspace (the _ws entry points, rows of at least 64 chunks), step (c) instead reads
-// chunk summaries written by summary_kernel just before: per full chunk, a 2048-slot table of
+// With a workspace (the _ws entry points, rows of at least 64 chunks), step (c) of chunks with
+// at most 512 distinct query codes instead reads chunk summaries written by summary_kernel
+// just before (chunks of more keep the queued scan of resolve_core.h): per full chunk, a 2048-slot table of
 // (fingerprint, latest position) per distinct key code. Only the query codes with no earlier
 // key in their own chunk (about 300 of 1024 positions' codes on Zipf data) probe the earlier
 // chunks' tables, latest first, 8 chunks per round trip, and every candidate is confirmed

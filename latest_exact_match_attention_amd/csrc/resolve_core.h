@@ -64,8 +64,8 @@ static_assert(kChunk / 64 <= 16, "word summary is a 16-bit mask");
 // seldom repeat (pre-activation codes of a language model) then cost one 4-byte LDS read
 // each. LEMA_RESOLVE_FILTER: 0 never, 1 always, 2 in chunks of more than kFilterMinCodes
 // distinct query codes (on Zipf-distributed codes, ~370 per chunk, the filter passes most
-// keys and only adds a read). Chunks that scan through the wider filter below (no chunk
-// summaries) use that one for their own keys too and do not build this one.
+// keys and only adds a read). Chunks with the filter scan their earlier keys through the
+// wider filter below, use that one for their own keys too, and do not build this one.
 #ifndef LEMA_RESOLVE_FILTER
 #define LEMA_RESOLVE_FILTER 2
 #endif
@@ -79,6 +79,15 @@ __device__ __forceinline__ uint32_t filter_hash(uint32_t h) { return (h * 0x2C1B
 constexpr int kWideBits = 32768;
 constexpr int kQueueCap = 384;
 constexpr int kScanGroup = 4;  // key batches whose loads the queued scan issues together
+// With chunk summaries, a chunk with the filter still scans through the queue, ignoring the
+// summaries, when more than this many of its codes are distinct. Codes that nearly never repeat
+// (uniform codes: 1014-1024 distinct per chunk) leave almost every query without an in-chunk
+// answer and without an early hit in the summaries, and probing every earlier chunk's summary
+// for each of them cost 5-6.5x the queued scan (32 rows x T = 65536: 701 against 129 us;
+// 16 x 262144: 3431 against 526 us). Zipf codes over 4096 values (585-668 distinct per chunk)
+// find their latest key a few chunks back, where the summaries win (16 x 262144: 441 against
+// 879 us).
+constexpr int kQueueSummMinCodes = 896;
 // The scan tests every earlier key with it, so it avoids the quarter-rate 32-bit multiply:
 // the high half is folded into the low 24 bits, which a full-rate 24-bit multiply mixes.
 // (__umul24 is declared to return int: the product is shifted as unsigned.)
@@ -636,11 +645,14 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
   const bool filt = LEMA_RESOLVE_FILTER == 1 || (LEMA_RESOLVE_FILTER == 2 && s.nq > kFilterMinCodes);
   // The rest is compiled twice, with and without the filter, so that chunks without it run
   // the code they ran before it existed.
-  auto rest = [&](auto filter_on) {
+  auto rest = [&](auto filter_on, auto queue_on) {
     constexpr bool kFilt = decltype(filter_on)::value;
     // Chunks with the filter scan the earlier keys first, through a wider filter, queueing the
     // few keys that pass (see below); the map and word summaries lend it their LDS meanwhile.
-    constexpr bool kQueue = kFilt && !kSumm;
+    // Where chunk summaries exist, only chunks of nearly all distinct codes do (see
+    // kQueueSummMinCodes).
+    constexpr bool kQueue = decltype(queue_on)::value;
+    static_assert(kFilt || !kQueue, "the queued scan needs the filter's chunk");
     uint32_t* wide = reinterpret_cast<uint32_t*>(s.summ);  // kWideBits, while kQueue scans
     if constexpr (kFilt) {
 #pragma unroll
@@ -914,7 +926,7 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       for (int p = 0; p < kPer; ++p)
         if (second[p]) src[p] += 63 - __clzll(s.mbits[m2[p]]);
     }
-    if (kSumm && chunk > 0) {
+    if (kSumm && !kQueue && chunk > 0) {
       // Summary path: the codes some query needs from before the chunk are listed (in the key
       // map's storage, dead by now) and each is looked up in the earlier chunks' summaries.
 #pragma unroll
@@ -947,10 +959,16 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       }
     }
   };
-  if (filt)
-    rest(std::true_type{});
-  else
-    rest(std::false_type{});
+  if (!filt) {
+    rest(std::false_type{}, std::false_type{});
+  } else if constexpr (kSumm) {
+    if (s.nq > kQueueSummMinCodes)
+      rest(std::true_type{}, std::true_type{});
+    else
+      rest(std::true_type{}, std::false_type{});
+  } else {
+    rest(std::true_type{}, std::true_type{});
+  }
 }
 
 }  // namespace

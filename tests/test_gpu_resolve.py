@@ -432,19 +432,23 @@ LONG = 64 * 1024 + 464          # rows of 65 chunks (ragged last chunk) take the
 def test_summary_path_equals_scan(dev, T, code_dtype):
     """Rows at the summaries' threshold (64 chunks) and past it, ragged last chunk included:
     both paths equal the oracle, on few-code rows (matches within a chunk), many-code rows
-    (matches across chunks) and far copies (matches many chunks back)."""
+    (matches across chunks; past the threshold these chunks scan through the queue), far
+    copies (matches many chunks back) and rows of ~690 distinct codes per chunk (the filter's
+    chunks that still read the summaries)."""
     from latest_exact_match_attention_amd import _lib
-    assert (_lib.lib().lema_resolve_workspace_bytes(4, T) > 0) == (T > 63 * 1024)
+    assert (_lib.lib().lema_resolve_workspace_bytes(5, T) > 0) == (T > 63 * 1024)
     rng = np.random.default_rng(T)
     rows = [rng.integers(0, 7, T), rng.integers(0, 30000, T), rng.integers(-2, 2, T)]
     far = rng.integers(0, 1 << 31, T)
     far[T // 2:] = far[:T - T // 2]          # every key of the second half repeats one
     rows.append(far)
+    rows.append(rng.integers(0, 1200, T))
     kc = np.stack(rows)
     i = np.arange(T)
     # row 3: query i >= T/2 asks for the key of i - T/2 (its copy at i itself is not < i)
     q3 = np.where(i >= T // 2, far[np.maximum(i - T // 2, 0)], rng.integers(0, 1 << 31, T))
-    qc = np.stack([rng.integers(0, 7, T), rng.integers(0, 30000, T), rng.integers(-2, 2, T), q3])
+    qc = np.stack([rng.integers(0, 7, T), rng.integers(0, 30000, T), rng.integers(-2, 2, T), q3,
+                   rng.integers(0, 1200, T)])
     want = both_paths(qc, kc, dev, code_dtype)
     assert (want[3] >= 0).mean() > 0.4
 
