@@ -18,8 +18,11 @@ The untimed warm-up runs the W steps asked for and continues until 0.5 s of laun
 
 `roofline` prices the fused kernel's algorithmic bytes against MI355X's 8 TB/s HBM peak,
 with the kernel time measured by HIP events on the stream it is launched on. `traffic` is
-the HBM bytes per launch from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed in
-profiles/ (null if absent). `cpu_baseline` times the reference's sort-based CPU algorithm
+the L2-miss bytes per launch (served by HBM or the 256 MB Infinity Cache) from the rocprofv3
+FETCH_SIZE/WRITE_SIZE summary committed in profiles/ (null if absent). Back-to-back launches
+over the same batch find part of it in the Infinity Cache; `cold_cache` times the same
+launch, and the same device copy, each after a read of a 1 GiB buffer that evicts L2 and the
+Infinity Cache. `cpu_baseline` times the reference's sort-based CPU algorithm
 (torch ops on the host's cores) on a bounded sample of the same workload.
 
 decode: batched decode against the HBM store -- 16 sequences x 64 heads = 1024 partitions,
@@ -36,7 +39,8 @@ d_model 1536, 64 heads (d_qk = d_v = 24, 24-bit codes), SwiGLU 6144, bf16, rando
 cross-entropy; `value` = tokens per second. The projections, MLP and head are bf16 GEMMs on
 the matrix cores (torch); each layer's exact op is the fused HIP kernel. `roofline` prices
 the step's GEMM FLOPs against the dense bf16 MFMA peak; `lema_kernel` gives the fused op's
-own HBM fraction at the layer shape. `cpu_baseline` runs the model forward restated in torch
+own HBM fraction at the layer shape, back to back on layer 0's codes and after the cache
+eviction of the prefill line (inside the forward it runs between other kernels' traffic). `cpu_baseline` runs the model forward restated in torch
 with the reference's sort-based exact op on the host's cores, fp32, on a short sample.
 
 long_context: B1 H64, T = 2^24 fed through the HBM store in 16 calls of 2^20 positions
@@ -221,9 +225,12 @@ def bench_prefill(a):
     hits = float((src >= 0).float().mean().item())
     nq = B * H * T
     achieved = BYTES_PER_QUERY * nq / (ms * 1e-3) / 1e9
-    # after the timed region; both overwrite y
+    # after the timed region; the copies overwrite y
+    cold = cold_ms(lambda: launch_hard(qd, kd, vd, y, src), stream)
     copy_gbps = measured_copy_gbps(vd, y, stream, lib_copy=True)
     torch_copy_gbps = measured_copy_gbps(vd, y, stream)
+    copy_cold = measured_copy_gbps(vd, y, stream, lib_copy=True, cold=True)
+    achieved_cold = BYTES_PER_QUERY * nq / (cold * 1e-3) / 1e9
     cpu = None if a.no_cpu_baseline else cpu_baseline_prefill(qc, kc, v32, a.cpu_rows)
     return {
         "metric": "prefill matched queries/sec @T=16k; decode steps/sec; % of HBM peak",
@@ -252,14 +259,56 @@ def bench_prefill(a):
                                                f"write {2 * vd.numel() * vd.element_size()} "
                                                "bytes), HIP events, median of 20",
                                        "torch_copy_GBps": torch_copy_gbps}},
+        "cold_cache": {"ms_per_step": cold, "value": nq / (cold * 1e-3),
+                       "achieved_GBps": achieved_cold, "frac": achieved_cold / HBM_PEAK_GBS,
+                       "copy_GBps": copy_cold, "copy_frac": achieved_cold / copy_cold,
+                       "what": f"each launch (and each copy) timed alone by HIP events after a "
+                               f"read of {FLUSH_BYTES >> 30} GiB that evicts L2 and the Infinity "
+                               f"Cache; median of {COLD_REPS}"},
         "cpu_baseline": cpu,
     }
 
 
-def measured_copy_gbps(src, dst, stream, reps: int = 20, lib_copy: bool = False) -> float:
+FLUSH_BYTES = 1 << 30   # larger than L2 (8 x 4 MB) and the Infinity Cache (256 MB) together
+COLD_REPS = 15
+_flush = {}
+
+
+def evict_caches(stream) -> None:
+    """Read FLUSH_BYTES of device memory (a float32 sum, nothing large written), so that what
+    runs next finds none of its data in L2 or the Infinity Cache."""
+    import torch
+    dev = stream.device
+    if dev not in _flush:
+        _flush[dev] = (torch.ones(FLUSH_BYTES // 2, dtype=torch.bfloat16, device=dev),
+                       torch.empty((), dtype=torch.float32, device=dev))
+    buf, acc = _flush[dev]
+    torch.sum(buf, dim=(0,), dtype=torch.float32, out=acc)
+
+
+def cold_ms(run, stream, reps: int = COLD_REPS) -> float:
+    """Median time (ms) of run() by HIP events, each call right after evict_caches."""
+    import torch
+    run()
+    times = []
+    for _ in range(reps):
+        evict_caches(stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def measured_copy_gbps(src, dst, stream, reps: int = 20, lib_copy: bool = False,
+                       cold: bool = False) -> float:
     """A device copy's rate on this GPU (bytes read + written per second, GB/s): the streaming
     rate HBM actually reaches, beside the 8 TB/s specification. lib_copy: the library's
-    lema_device_copy (consecutive workgroups on consecutive 32 KB regions), else torch's."""
+    lema_device_copy (consecutive workgroups on consecutive 32 KB regions), else torch's.
+    cold: each copy timed after evict_caches (median of COLD_REPS)."""
     import torch
     from latest_exact_match_attention_amd import _lib
     nbytes = src.numel() * src.element_size()
@@ -270,6 +319,8 @@ def measured_copy_gbps(src, dst, stream, reps: int = 20, lib_copy: bool = False)
                                                    stream.cuda_stream))
         else:
             dst.copy_(src)
+    if cold:
+        return 2 * nbytes / (cold_ms(run, stream) * 1e-3) / 1e9
     for _ in range(3):
         run()
     torch.cuda.synchronize()
@@ -567,6 +618,7 @@ def bench_lm(a):
         e1.record(stream)
         torch.cuda.synchronize()
         ms_l = e0.elapsed_time(e1) / n_l
+        ms_lc = cold_ms(lambda: launch_hard(qc, kc, v, yv), stream)
         src = torch.empty((B, cfg.num_heads, T), dtype=torch.int32, device=dev)
         launch_hard(qc, kc, v, yv, src)
         hits = float((src >= 0).float().mean())
@@ -606,8 +658,10 @@ def bench_lm(a):
                      "flops_per_token": lm_flops_per_token(cfg)},
         "lema_kernel": {"kernel": "resolve_lag_kernel (fused resolve + gather), one layer",
                         "us": ms_l * 1e3, "queries": nq, "bytes_per_query": bpq,
-                        "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS},
-        "pack_kernel": {"kernel": "pack_dense_kernel, one layer's query codes",
+                        "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS,
+                        "us_cold_cache": ms_lc * 1e3,
+                        "frac_cold_cache": bpq * nq / (ms_lc * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "pack_kernel": {"kernel": "pack_tile_kernel, one layer's query codes",
                         "us": ms_p * 1e3, "rows": nq, "bytes_per_row": 2 * cfg.d_qk + 4,
                         "achieved_gbs": (2 * cfg.d_qk + 4) * nq / (ms_p * 1e-3) / 1e9,
                         "frac": (2 * cfg.d_qk + 4) * nq / (ms_p * 1e-3) / 1e9 / HBM_PEAK_GBS},
