@@ -156,22 +156,24 @@ __global__ __launch_bounds__(kPackThreads) void pack_dense_kernel(DenseArgs a) {
 
 // Rows of 64 heads innermost in memory (the [B, T, H * D] projection viewed as [B, H, T, D])
 // whose codes go to [B, H, T]: a wavefront's 64 codes would land T apart. A workgroup packs
-// 32 consecutive row groups (positions) instead, 8 per wavefront, stages the [32][64] codes in
-// LDS and writes each head's 32 positions as one contiguous run.
-constexpr int kTileGroups = 32;
-template <int DTYPE, typename CodeT>
+// G consecutive row groups (positions) instead, G / 4 per wavefront, stages the [G][64] codes
+// in LDS and writes each head's G positions as one contiguous run. G = 16 on inputs of 2^21
+// rows or more, 8 below, so that smaller inputs still spread over the whole GPU (one LM layer,
+// B4 H64 T16384 d 24: 36-37 us with 8 or 16, 37.9 with 32; B1 H64 T1000: 4.3 us with 8,
+// 6.0 with 16, 10.0 with 32; a read of the same bytes alone takes 33.3 and 4.4 us).
+template <int DTYPE, typename CodeT, int G>
 __global__ __launch_bounds__(kPackThreads) void pack_tile_kernel(DenseArgs a) {
   __shared__ uint64_t words[kPackThreads / 64][64 + 1];
-  __shared__ CodeT tile[kTileGroups][64 + 1];
+  __shared__ CodeT tile[G][64 + 1];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTileGroups * 64;
-  for (int g = w; g < kTileGroups; g += kPackThreads / 64) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * G * 64;
+  for (int g = w; g < G; g += kPackThreads / 64) {
     const int64_t m0 = base + static_cast<int64_t>(g) * 64;
     if (m0 < a.R) tile[g][lane] = static_cast<CodeT>(row_code<DTYPE>(a, words[w], m0, lane));
   }
   __syncthreads();
-  for (int idx = t; idx < kTileGroups * 64; idx += kPackThreads) {
-    const int h = idx / kTileGroups, g = idx % kTileGroups;  // consecutive threads: positions
+  for (int idx = t; idx < G * 64; idx += kPackThreads) {
+    const int h = idx / G, g = idx % G;  // consecutive threads: positions
     const int64_t m = base + static_cast<int64_t>(g) * 64 + h;
     if (m < a.R) static_cast<CodeT*>(a.codes)[out_index(a, m)] = tile[g][h];
   }
@@ -199,18 +201,23 @@ __global__ __launch_bounds__(kPackThreads) void pack_strided_kernel(StridedArgs 
   static_cast<CodeT*>(a.codes)[r] = static_cast<CodeT>(code);
 }
 
+template <typename CodeT, int G>
+int launch_tile(int32_t dtype, const DenseArgs& a, hipStream_t st) {
+  const int64_t grid = (a.R + G * 64 - 1) / (G * 64);
+  LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
+  switch (dtype) {
+    case LEMA_F32: pack_tile_kernel<LEMA_F32, CodeT, G><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    case LEMA_F16: pack_tile_kernel<LEMA_F16, CodeT, G><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+    default: pack_tile_kernel<LEMA_BF16, CodeT, G><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
+  }
+  return launch_status("pack_tile_kernel");
+}
+
 template <typename CodeT>
 int launch_dense(int32_t dtype, const DenseArgs& a, hipStream_t st) {
-  if (a.E2 == 64 && a.os1 == 1 && a.os2 != 1) {  // 64 heads innermost, positions contiguous out
-    const int64_t grid = (a.R + kTileGroups * 64 - 1) / (kTileGroups * 64);
-    LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
-    switch (dtype) {
-      case LEMA_F32: pack_tile_kernel<LEMA_F32, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
-      case LEMA_F16: pack_tile_kernel<LEMA_F16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
-      default: pack_tile_kernel<LEMA_BF16, CodeT><<<dim3(grid), dim3(kPackThreads), 0, st>>>(a); break;
-    }
-    return launch_status("pack_tile_kernel");
-  }
+  if (a.E2 == 64 && a.os1 == 1 && a.os2 != 1)  // 64 heads innermost, positions contiguous out
+    return a.R >= (int64_t(1) << 21) ? launch_tile<CodeT, 16>(dtype, a, st)
+                                     : launch_tile<CodeT, 8>(dtype, a, st);
   const int64_t grid = (a.R + kPackThreads - 1) / kPackThreads;
   LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many rows to pack");
   switch (dtype) {

@@ -93,6 +93,23 @@ def test_pack_layouts(dev, D, dtype, layout, H):
         assert np.array_equal(got32.astype(np.uint64), want)
 
 
+@pytest.mark.parametrize("D,code_dtype", [(24, torch.int32), (64, torch.int64)])
+def test_pack_projection_large(dev, D, code_dtype):
+    """The tiled kernel's larger tiles (inputs of 2^21 rows or more): B1 H64 T32845 in the
+    projection layout, the last tile partial."""
+    B, H, T = 1, 64, 32845
+    assert B * H * T >= 1 << 21
+    gen = torch.Generator(device="cpu").manual_seed(D)
+    base = torch.randn(B, T, H * D, generator=gen).to(torch.bfloat16)
+    base.view(-1)[:5] = torch.tensor([0.0, -0.0, float("nan"), float("inf"), -float("inf")]).to(torch.bfloat16)
+    zd = base.to(dev).view(B, T, H, D).transpose(1, 2)
+    carrier = base.view(B, T, H, D).transpose(1, 2).contiguous().view(torch.int16).numpy().view(np.uint16)
+    want = oracle.pack_codes(carrier, "bf16")
+    got = pack_codes(zd, code_dtype).cpu().numpy()
+    got = got.view(np.uint32).astype(np.uint64) if code_dtype == torch.int32 else got.view(np.uint64)
+    assert np.array_equal(got, want)
+
+
 def test_pack_generic_shape(dev):
     z = torch.randn(5, 7, 3, 9, 12)
     got = pack_codes(z.to(dev)).cpu().numpy().view(np.uint64)
