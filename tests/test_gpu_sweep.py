@@ -1,0 +1,123 @@
+"""A seeded sweep of the prefill path over mixed shapes, against the CPU oracle: each case draws
+batch, heads, length (around chunk boundaries of 1024 positions and the 64-chunk summary
+threshold), code alphabet and structure, code width, value width and dtype, the value layout
+(contiguous, or the [B, T, H * d_v] projection viewed as [B, H, T, d_v]) and the miss fill.
+Indices and value bits must equal the oracle's (code/lema/attention.py:100-158)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from latest_exact_match_attention_amd import gather_values, latest_prev_match, lema_from_codes
+
+LENGTHS = [1, 2, 63, 64, 1000, 1023, 1024, 1025, 2047, 2048, 3000, 5121, 16383, 16385,
+           40000, 64 * 1024 - 1024, 64 * 1024 + 5]
+TORCH = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+NP_CARRIER = {"f32": np.float32, "bf16": np.uint16, "f16": np.uint16}
+
+
+def draw_case(seed: int) -> dict:
+    rng = np.random.default_rng(seed)
+    T = int(rng.choice(LENGTHS))
+    H = int(rng.choice([1, 3, 8, 64]))
+    B = int(rng.choice([1, 2, 3]))
+    while B * H * T > 3_000_000 and (B > 1 or H > 1):   # the oracle stays within seconds
+        if B > 1:
+            B -= 1
+        else:
+            H = max(1, H // 4)
+    dv = int(rng.choice([1, 2, 7, 16, 24, 64, 130]))
+    while B * H * T * dv > 12_000_000 and (B > 1 or H > 1):   # host copies stay small
+        if B > 1:
+            B -= 1
+        else:
+            H = max(1, H // 4)
+    code_bytes = int(rng.choice([4, 8]))
+    alphabet = int(rng.choice([2, 40, 1000, max(2, T // 2), 1 << 24]
+                              + ([1 << 40, 1 << 63] if code_bytes == 8 else [])))
+    return {"seed": seed, "B": B, "H": H, "T": T, "code_bytes": code_bytes, "alphabet": alphabet,
+            "structure": str(rng.choice(["uniform", "zipf", "runs"])),
+            "dv": dv,
+            "dtype": str(rng.choice(["f32", "bf16", "f16"])),
+            "layout": str(rng.choice(["contiguous", "projection"])),
+            "src_dtype": (torch.int32, torch.int64)[int(rng.integers(0, 2))]}
+
+
+def draw_codes(rng, case, shape) -> np.ndarray:
+    a = case["alphabet"]
+    if case["structure"] == "zipf":
+        c = rng.zipf(1.2, size=shape) - 1
+        if a <= (1 << 62):                # larger alphabets hold every drawn value
+            c %= a
+    elif case["structure"] == "runs":   # long runs of one code: many hits at distance 1
+        c = np.repeat(rng.integers(0, a, size=shape[:-1] + (shape[-1] // 16 + 1,)), 16,
+                      axis=-1)[..., :shape[-1]]
+    else:
+        c = rng.integers(0, a, size=shape, dtype=np.uint64 if a > (1 << 62) else np.int64)
+    c = c.astype(np.uint64)
+    if case["code_bytes"] == 4:
+        return c.astype(np.uint32).view(np.int32)
+    return c.view(np.int64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(96))
+def test_prefill_sweep(dev, seed):
+    case = draw_case(1000 + seed)
+    print("case", case, flush=True)
+    rng = np.random.default_rng(case["seed"])
+    B, H, T, dv = case["B"], case["H"], case["T"], case["dv"]
+    qc = draw_codes(rng, case, (B, H, T))
+    kc = draw_codes(rng, case, (B, H, T))
+    if rng.random() < 0.5:              # queries drawn from the keys: more hits
+        kc = np.where(rng.random((B, H, T)) < 0.5, qc, kc)
+    v32 = rng.standard_normal((B, H, T, dv)).astype(np.float32)
+    v32[:, :, 0, 0] = -0.0
+    dt = case["dtype"]
+    tdt = TORCH[dt]
+    if case["layout"] == "projection":
+        base = torch.from_numpy(np.ascontiguousarray(v32.transpose(0, 2, 1, 3))).to(tdt)
+        v = base.reshape(B, T, H * dv).to(dev).view(B, T, H, dv).transpose(1, 2)
+    else:
+        v = torch.from_numpy(v32).to(tdt).to(dev)
+    q, k = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+
+    want_src = oracle.latest_prev_match(qc.reshape(B * H, T), kc.reshape(B * H, T))
+    src = latest_prev_match(q.view(B * H, T), k.view(B * H, T), out_dtype=case["src_dtype"])
+    assert np.array_equal(src.cpu().numpy().astype(np.int64), want_src)
+
+    vc = v.contiguous().cpu()
+    carrier = (vc.numpy() if dt == "f32" else
+               vc.view(torch.int16).numpy().view(np.uint16)).reshape(B * H, T, dv)
+    y, src32 = lema_from_codes(q, k, v, return_src=True)
+    assert np.array_equal(src32.cpu().numpy().reshape(B * H, T), want_src)
+    got = y.contiguous().cpu()
+    got = (got.numpy() if dt == "f32" else got.view(torch.int16).numpy().view(np.uint16))
+    want = oracle.gather(carrier, dt, want_src, 0)
+    assert _same(got.reshape(want.shape), want, dt)
+
+    yz = gather_values(v, src.view(B, H, T), miss="zero").contiguous().cpu()
+    yz = (yz.numpy() if dt == "f32" else yz.view(torch.int16).numpy().view(np.uint16))
+    want = oracle.gather(carrier, dt, want_src, 1)
+    assert _same(yz.reshape(want.shape), want, dt)
+
+
+def _same(got: np.ndarray, want: np.ndarray, dtype: str) -> bool:
+    """Bitwise equality (the sweep's values hold no NaN; -0 is compared by its bits)."""
+    return bool(np.array_equal(got.view(NP_CARRIER[dtype]), want.view(NP_CARRIER[dtype])))
+
+
+def test_sweep_covers_the_paths():
+    """The drawn cases reach long rows (chunk summaries), rows of one chunk, both code widths,
+    every dtype and layout, lengths that end inside a chunk, and launches of more items than
+    the GPU holds workgroups."""
+    cases = [draw_case(1000 + s) for s in range(96)]
+    assert any(c["T"] >= 64 * 1024 for c in cases)
+    assert any(c["T"] <= 1024 for c in cases)
+    assert any(c["T"] % 1024 not in (0,) and c["T"] > 1024 for c in cases)
+    assert {c["code_bytes"] for c in cases} == {4, 8}
+    assert {c["dtype"] for c in cases} == {"f32", "bf16", "f16"}
+    assert {c["layout"] for c in cases} == {"contiguous", "projection"}
+    assert any(c["layout"] == "projection" and c["H"] == 64 for c in cases)
+    # more (row, chunk) items than the GPU holds workgroups: the persistent kernel
+    assert sum(c["B"] * c["H"] * -(-c["T"] // 1024) > 1024 for c in cases) >= 2
