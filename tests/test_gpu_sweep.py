@@ -1,8 +1,15 @@
-"""A seeded sweep of the prefill path over mixed shapes, against the CPU oracle: each case draws
-batch, heads, length (around chunk boundaries of 1024 positions and the 64-chunk summary
-threshold), code alphabet and structure, code width, value width and dtype, the value layout
-(contiguous, or the [B, T, H * d_v] projection viewed as [B, H, T, d_v]) and the miss fill.
-Indices and value bits must equal the oracle's (code/lema/attention.py:100-158)."""
+"""Seeded sweeps over mixed shapes, against the CPU oracle.
+
+Prefill: each case draws batch, heads, length (around chunk boundaries of 1024 positions and
+the 64-chunk summary threshold), code alphabet and structure, code width, value width and
+dtype, the value layout (contiguous, or the [B, T, H * d_v] projection viewed as [B, H, T,
+d_v]) and the miss fill. Indices and value bits must equal the oracle's
+(code/lema/attention.py:100-158).
+
+Store: each case draws partitions, a sequence of exchanges over group ranges (decode-sized,
+chunked and bulk calls, some insert-only), code width and alphabet with codes 0 and all-ones,
+value row width and the final load; outputs, counts and table content must equal one dict per
+partition (code/tests/test_store.py:17-41)."""
 import numpy as np
 import pytest
 import torch
@@ -121,3 +128,92 @@ def test_sweep_covers_the_paths():
     assert any(c["layout"] == "projection" and c["H"] == 64 for c in cases)
     # more (row, chunk) items than the GPU holds workgroups: the persistent kernel
     assert sum(c["B"] * c["H"] * -(-c["T"] // 1024) > 1024 for c in cases) >= 2
+
+
+# ------------------------------------------------------------------------------ the store
+STORE_CALL_T = [1, 1, 2, 100, 1024, 1025, 1500, 2049, 3000, 5000]
+
+
+def draw_store_case(seed: int) -> dict:
+    """Partitions, a sequence of exchanges (group range, positions per partition, insert-only or
+    not), code width and alphabet, value row width and the table's load after the last call."""
+    rng = np.random.default_rng(seed)
+    P = int(rng.choice([1, 5, 64, 200]))
+    calls, items = [], 0
+    if P == 200 and rng.random() < 0.5:   # a long call over many partitions: the bulk path
+        calls.append((0, P, 3000, False))
+        items += P * 3000
+    while len(calls) < 6 and items < 100_000:
+        T = int(rng.choice(STORE_CALL_T))
+        g0 = int(rng.integers(0, P))
+        Pc = int(rng.integers(1, P - g0 + 1))
+        if Pc * T > 650_000:               # the dict oracle stays within about a second
+            Pc = max(1, 650_000 // T)
+        calls.append((g0, Pc, T, bool(rng.random() < 0.2)))
+        items += Pc * T
+    code_bytes = int(rng.choice([4, 8]))
+    alphabet = int(rng.choice([3, 50, 1000, 1 << 20] + ([1 << 62] if code_bytes == 8 else
+                                                       [1 << 31])))
+    return {"seed": seed, "P": P, "calls": calls, "code_bytes": code_bytes, "alphabet": alphabet,
+            "d_v": int(rng.choice([4, 8, 12, 24, 64])), "load": float(rng.choice([0.3, 0.7, 0.85]))}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(32))
+def test_store_sweep(dev, seed):
+    """Every exchange's output, the counts per partition and the final table content against
+    one dict per partition with latest-write-wins (code/tests/test_store.py:17-41), codes 0 and
+    all-ones included, 32-bit codes compared as their 32-bit patterns."""
+    from latest_exact_match_attention_amd.cache import HashStore
+    case = draw_store_case(5000 + seed)
+    print("case", case, flush=True)
+    rng = np.random.default_rng(case["seed"])
+    P, d_v, cb = case["P"], case["d_v"], case["code_bytes"]
+    mask = (1 << 32) - 1 if cb == 4 else (1 << 64) - 1
+    data = []
+    for g0, Pc, T, insert_only in case["calls"]:
+        n = Pc * T
+        qc = rng.integers(0, case["alphabet"], size=n, dtype=np.int64).astype(np.uint64)
+        kc = rng.integers(0, case["alphabet"], size=n, dtype=np.int64).astype(np.uint64)
+        for c in (qc, kc):                # the two codes a table could mistake for markers
+            c[rng.random(n) < 0.01] = 0
+            c[rng.random(n) < 0.01] = mask
+        vals = rng.integers(0, 1 << 16, size=(n, d_v), dtype=np.uint16)
+        data.append((qc, kc, vals))
+    keys = set()
+    for (g0, Pc, T, _), (_, kc, _) in zip(case["calls"], data):
+        keys.update(zip((g0 + np.arange(kc.size) // T).tolist(), kc.tolist()))
+    cap = max(64, int(len(keys) / case["load"]) + 1)
+    store = HashStore(d_v, groups=P, dtype=np.uint16, capacity=cap, device=dev)
+    ref = oracle.DictStore(P, 2 * d_v)
+    for (g0, Pc, T, insert_only), (qc, kc, vals) in zip(case["calls"], data):
+        to_dev = (lambda c: torch.from_numpy(c.astype(np.uint32).view(np.int32)).to(dev)) \
+            if cb == 4 else (lambda c: torch.from_numpy(c.view(np.int64)).to(dev))
+        out = None if insert_only else torch.empty((qc.size, d_v), dtype=torch.int16, device=dev)
+        store.exchange(None if insert_only else to_dev(qc), to_dev(kc),
+                       torch.from_numpy(vals.view(np.int16)).to(dev), out, T, g0)
+        want = ref.exchange(qc, kc, vals.view(np.uint8).reshape(-1, 2 * d_v), T, g0)
+        if not insert_only:
+            got = out.cpu().numpy().view(np.uint8).reshape(-1, 2 * d_v)
+            assert np.array_equal(got, want), (g0, Pc, T)
+    assert np.array_equal(store.counts.numpy(), ref.counts())
+    grp, code, val = store.dump()
+    got = {(int(a), int(b) & mask): bytes(c) for a, b, c in
+           zip(grp.cpu().numpy(), code.cpu().numpy(), val.cpu().numpy())}
+    want = {(p, k): bytes(v) for p, d in enumerate(ref.ref) for k, v in d.items()}
+    assert got == want
+
+
+def test_store_sweep_covers_the_paths():
+    """The drawn store cases reach decode-sized calls, the chunked path and the bulk path (long
+    calls over few and over many partitions), insert-only calls, both code widths and loads of
+    0.85."""
+    cases = [draw_store_case(5000 + s) for s in range(32)]
+    calls = [c for case in cases for c in case["calls"]]
+    assert any(T == 1 for _, _, T, _ in calls)
+    assert any(1 < T <= 1024 for _, _, T, _ in calls)
+    assert any(T > 1024 and Pc <= 128 for _, Pc, T, _ in calls)
+    assert any(T > 2048 and Pc > 128 for _, Pc, T, _ in calls)
+    assert any(io for _, _, _, io in calls)
+    assert {c["code_bytes"] for c in cases} == {4, 8}
+    assert any(c["load"] == 0.85 for c in cases)
