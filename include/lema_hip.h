@@ -36,6 +36,7 @@ enum lema_miss { LEMA_MISS_DENSE = 0, /* v[b, h, 0, :] * 0: a signed zero, NaN f
                  LEMA_MISS_ZERO = 1 /* +0 bytes, the store path */ };
 
 const char* lema_last_error(void);
+/* The version of this C ABI (1). No counterpart in the reference. */
 int lema_abi_version(void);
 
 /* dst[0, bytes) = src[0, bytes) on the device (bytes a multiple of 16, both pointers 16-byte
