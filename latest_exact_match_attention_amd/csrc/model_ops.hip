@@ -65,30 +65,44 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const u
 
 // One workgroup (256 threads) per row of V bf16 logits (V % 8 == 0, rows 16-byte aligned):
 // each thread keeps a running max and a sum rescaled to it, then the workgroup combines them.
+// Each trip loads two 16-byte pieces (both in flight), and e^(x - m) is 2^(x log2 e - m log2 e):
+// one FMA and the hardware base-2 exponential per logit. With expf per logit and one load per
+// trip the kernel was bound by VALU issue: 4096 x 50304 logits took 114-133 us, now 75 us
+// (5.4 TB/s), at the same error against an fp32 cross-entropy (about 2e-7 per row).
 __global__ __launch_bounds__(256) void xent_kernel(const uint16_t* logits, int64_t V, int64_t ld,
                                                    const int64_t* target, float* loss) {
   __shared__ float smax[4], ssum[4];
+  constexpr float kLog2e = 1.4426950408889634f;
   const int64_t row = blockIdx.x;
   const uint16_t* r = logits + row * ld;
   float m = -INFINITY, s = 0.0f;
-  for (int64_t e = static_cast<int64_t>(threadIdx.x) * 8; e < V; e += 256 * 8) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(r + e);
-    const uint32_t* pv = reinterpret_cast<const uint32_t*>(&v);
-    float x[8];
+  for (int64_t e0 = static_cast<int64_t>(threadIdx.x) * 8; e0 < V; e0 += 2 * 256 * 8) {
+    const int64_t e1 = e0 + 256 * 8;
+    const bool two = e1 < V;
+    const u32x4 va = *reinterpret_cast<const u32x4*>(r + e0);
+    u32x4 vb = va;  // a repeat of the first piece when the second lies past the row
+    if (two) vb = *reinterpret_cast<const u32x4*>(r + e1);
+    const uint32_t pv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+    float x[16];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 8; ++k) {
       x[2 * k] = bf16_to_f32(pv[k] & 0xFFFFu);
       x[2 * k + 1] = bf16_to_f32(pv[k] >> 16);
     }
     float bm = x[0];
 #pragma unroll
-    for (int k = 1; k < 8; ++k) bm = fmaxf(bm, x[k]);
+    for (int k = 1; k < 16; ++k) bm = fmaxf(bm, x[k]);
     if (bm > m) {
-      s *= expf(m - bm);
+      s *= __builtin_amdgcn_exp2f((m - bm) * kLog2e);
       m = bm;
     }
+    const float mb = m * kLog2e;
+    float sa = 0.0f, sb = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s += expf(x[k] - m);
+    for (int k = 0; k < 8; ++k) sa += __builtin_amdgcn_exp2f(fmaf(x[k], kLog2e, -mb));
+#pragma unroll
+    for (int k = 8; k < 16; ++k) sb += __builtin_amdgcn_exp2f(fmaf(x[k], kLog2e, -mb));
+    s += two ? sa + sb : sa;
   }
   // combine: wavefront, then the 4 wavefronts
 #pragma unroll

@@ -57,6 +57,28 @@ def test_cross_entropy_from_bf16_logits(dev):
     assert abs(got.item() - want.item()) <= 1e-5 * abs(want.item())
 
 
+@pytest.mark.parametrize("V,scale", [(8, 4.0), (2056, 1.0), (8200, 30.0), (50304, 4.0)])
+def test_cross_entropy_rows(dev, V, scale):
+    """Every row's loss within 1e-6 of an fp32 cross-entropy, relative to the loss or to 1
+    where the loss is smaller (float32 rounding of log S + M - x_t): vocabularies that end
+    inside a thread's first or second piece, logits spread from 1 to 30 standard deviations,
+    and -inf logits (a masked entry adds nothing)."""
+    from latest_exact_match_attention_amd import _lib
+    g = torch.Generator(device=dev).manual_seed(V)
+    rows = 37
+    logits = (torch.randn(rows, V, device=dev, generator=g) * scale).to(torch.bfloat16)
+    y = torch.randint(0, V, (rows,), device=dev, generator=g)
+    logits[1, (y[1] + 1) % V] = -float("inf")
+    logits[2, :: 3] = -float("inf")
+    logits[2, y[2]] = 0.5
+    loss = torch.empty(rows, device=dev, dtype=torch.float32)
+    _lib.check(_lib.lib().lema_cross_entropy_bf16(logits.data_ptr(), rows, V, V, y.data_ptr(),
+                                                  loss.data_ptr(), _lib.stream_of(logits)))
+    want = F.cross_entropy(logits.float(), y, reduction="none")
+    rel = ((loss.double() - want.double()).abs() / want.double().abs().clamp_min(1.0)).max()
+    assert rel <= 1e-6, rel
+
+
 @pytest.mark.parametrize("rows", [1, 16, 33])
 @pytest.mark.parametrize("V", [50304, 8, 64, 8200])
 def test_argmax_equals_torch(dev, rows, V):
