@@ -37,13 +37,27 @@ __device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
   return out;
 }
 
+// Two 16-byte pieces of gate and of up per thread and trip, all four loads in flight before
+// the first product (one piece per trip: 447-522 us on [65536, 6144] over two GPUs; two:
+// 428-461 us, the same bits).
 __global__ __launch_bounds__(256) void swiglu_kernel(const u32x4* gate, const u32x4* up,
                                                      u32x4* out, int64_t n8) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const u32x4 g = gate[i], u = up[i];
-    out[i] = u32x4{swiglu_pair(g.x, u.x), swiglu_pair(g.y, u.y), swiglu_pair(g.z, u.z),
-                   swiglu_pair(g.w, u.w)};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i0 < n8;
+       i0 += 2 * stride) {
+    const int64_t i1 = i0 + stride;
+    const bool two = i1 < n8;
+    const u32x4 g0 = gate[i0], u0 = up[i0];
+    u32x4 g1 = g0, u1 = u0;
+    if (two) {
+      g1 = gate[i1];
+      u1 = up[i1];
+    }
+    out[i0] = u32x4{swiglu_pair(g0.x, u0.x), swiglu_pair(g0.y, u0.y), swiglu_pair(g0.z, u0.z),
+                    swiglu_pair(g0.w, u0.w)};
+    if (two)
+      out[i1] = u32x4{swiglu_pair(g1.x, u1.x), swiglu_pair(g1.y, u1.y), swiglu_pair(g1.z, u1.z),
+                      swiglu_pair(g1.w, u1.w)};
   }
 }
 
