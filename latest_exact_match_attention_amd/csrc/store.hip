@@ -61,6 +61,10 @@ static_assert(kGroup == 1 || kGroup == 2 || kGroup == 4 || kGroup == 8 || kGroup
               "probe group width");
 static_assert(kStepGroup == 8 || kStepGroup == 16 || kStepGroup == 32 || kStepGroup == 64,
               "probe group width");
+// A decode step on a table in host memory probes narrower windows: there each step is bound by
+// the host link's rate of small requests, not by round trips (1024 partitions at load 0.5:
+// 153.7 us per step with 32 lanes, 127.6 with 16, 125.9 with 8).
+constexpr int kStepGroupHost = 16;
 static_assert(kStepBlock % 64 == 0 && kStepBlock >= kStepGroup, "whole wavefronts of groups");
 
 __device__ __forceinline__ uint64_t splitmix_fin(uint64_t x) {
@@ -311,7 +315,7 @@ __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, con
   return -1;
 }
 
-// A decode step (T == 1): item i is partition i, kStepGroup lanes per item. Everything that does
+// A decode step (T == 1): item i is partition i, G lanes per item. Everything that does
 // not depend on the table is loaded up front (both codes, the item's value row when it fits one
 // 16-byte piece per lane); the query's first window is read as whole slots when they are small
 // enough (`spec`), so a hit needs no further read; after the windows only a claim (one CAS)
@@ -334,9 +338,9 @@ __device__ int group_insert(const StoreArgs& a, uint64_t code, uint64_t tag, con
   do {                \
   } while (0)
 #endif
+template <int G>
 __global__ __launch_bounds__(kStepBlock) void store_step_kernel(StoreArgs a) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  constexpr int G = kStepGroup;
   const int64_t i = gid / G;
   const int lane = threadIdx.x & 63, gl = lane % G, gbase = lane - gl;
   if (i >= a.n) return;  // whole groups only: n is a count of items, groups are aligned
@@ -1360,6 +1364,24 @@ int run_bulk(StoreArgs a, void* workspace, int64_t ws_bytes, hipStream_t st) {
   return LEMA_OK;
 }
 
+// Whether `table` is host memory (a pinned table the kernels reach over the host link). The
+// answer for the calling thread's last table is kept, so a run of decode steps asks HIP once;
+// a table freed and another allocated at the same address could only get the other window
+// width, never a wrong result. A pointer HIP does not know counts as device memory, and the
+// error the query leaves is cleared so that it is not reported for the next launch.
+bool table_in_host_memory(const void* table) {
+  static thread_local const void* last = nullptr;
+  static thread_local bool last_host = false;
+  if (table != last) {
+    hipPointerAttribute_t at{};
+    const hipError_t e = hipPointerGetAttributes(&at, table);
+    if (e != hipSuccess) (void)hipGetLastError();
+    last_host = e == hipSuccess && at.type == hipMemoryTypeHost;
+    last = table;
+  }
+  return last_host;
+}
+
 int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, const void* kc,
                    int32_t code_bytes, const void* values, void* out, int64_t n, int64_t T,
                    int64_t g0, int64_t* counts, int32_t* full, void* workspace, int64_t ws_bytes,
@@ -1404,17 +1426,23 @@ int store_exchange(void* table, int64_t cap, int64_t vbytes, const void* qc, con
                    (out == nullptr || aligned(out, 16));
   a.piece = p16 ? 16 : 8;
   a.pieces = static_cast<int32_t>(vbytes / a.piece);
-  a.pre = p16 && a.pieces <= kStepGroup;
+  a.pre = false;  // set for a decode step below
   a.spec = p16 && a.pieces <= kSpecPieces;
   a.cg_log2 = 0;
   while ((1 << a.cg_log2) < a.pieces && a.cg_log2 < 4) ++a.cg_log2;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t P = n / T;
   if (T == 1) {
-    const int64_t threads = n * kStepGroup;
+    const bool host = table_in_host_memory(table);
+    const int G = host ? kStepGroupHost : kStepGroup;
+    a.pre = p16 && a.pieces <= G;
+    const int64_t threads = n * G;
     const int64_t grid = (threads + kStepBlock - 1) / kStepBlock;
     LEMA_REQUIRE(grid < (int64_t(1) << 31), "too many items (%lld)", (long long)n);
-    store_step_kernel<<<dim3(grid), dim3(kStepBlock), 0, st>>>(a);
+    if (host)
+      store_step_kernel<kStepGroupHost><<<dim3(grid), dim3(kStepBlock), 0, st>>>(a);
+    else
+      store_step_kernel<kStepGroup><<<dim3(grid), dim3(kStepBlock), 0, st>>>(a);
     return launch_status("store_step_kernel");
   }
   LEMA_REQUIRE(P < (int64_t(1) << 31), "too many partitions (%lld)", (long long)P);
