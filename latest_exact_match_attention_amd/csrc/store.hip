@@ -65,7 +65,10 @@ static_assert(kStepGroup == 8 || kStepGroup == 16 || kStepGroup == 32 || kStepGr
 // the host link's rate of small requests, not by round trips (1024 partitions at load 0.5:
 // 153.7 us per step with 32 lanes, 127.6 with 16, 125.9 with 8).
 constexpr int kStepGroupHost = 16;
-static_assert(kStepBlock % 64 == 0 && kStepBlock >= kStepGroup, "whole wavefronts of groups");
+static_assert(kStepGroupHost == 8 || kStepGroupHost == 16 || kStepGroupHost == 32,
+              "probe group width");
+static_assert(kStepBlock % 64 == 0 && kStepBlock >= kStepGroup && kStepBlock >= kStepGroupHost,
+              "whole wavefronts of groups");
 
 __device__ __forceinline__ uint64_t splitmix_fin(uint64_t x) {
   x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
