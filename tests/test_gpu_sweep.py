@@ -1,5 +1,8 @@
 """Seeded sweeps over mixed shapes, against the CPU oracle.
 
+Sign-pack: each case draws heads, positions, width, dtype, layout and code width, some of them
+at 2^21 rows and more; codes must equal the oracle's (code/lema/attention.py:82-97).
+
 Prefill: each case draws batch, heads, length (around chunk boundaries of 1024 positions and
 the 64-chunk summary threshold), code alphabet and structure, code width, value width and
 dtype, the value layout (contiguous, or the [B, T, H * d_v] projection viewed as [B, H, T,
@@ -217,3 +220,62 @@ def test_store_sweep_covers_the_paths():
     assert any(io for _, _, _, io in calls)
     assert {c["code_bytes"] for c in cases} == {4, 8}
     assert any(c["load"] == 0.85 for c in cases)
+
+
+# ----------------------------------------------------------------------------- sign-pack
+def draw_pack_case(seed: int) -> dict:
+    """Heads, positions, width, dtype, layout (contiguous [B, H, T, D], or the projection
+    [B, T, H * D] viewed as [B, H, T, D]) and code width; some cases reach 2^21 rows, where
+    the 64-head projection view takes the tiled kernel's larger tiles."""
+    rng = np.random.default_rng(seed)
+    H = int(rng.choice([1, 5, 64]))
+    D = int(rng.choice([1, 7, 8, 16, 24, 31, 32, 40, 64]))
+    big = H == 64 and rng.random() < 0.4
+    T = int(rng.integers(32769, 34000)) if big else int(rng.choice([1, 63, 64, 65, 1000, 4097]))
+    B = 1 if big else int(rng.choice([1, 2, 3]))
+    return {"seed": seed, "B": B, "H": H, "T": T, "D": D,
+            "dtype": "bf16" if big else str(rng.choice(["f32", "bf16", "f16"])),
+            "layout": "projection" if big or (H == 64 and rng.random() < 0.7) else
+                      str(rng.choice(["contiguous", "projection"])),
+            "code_dtype": torch.int32 if D <= 32 and rng.random() < 0.5 else torch.int64}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(32))
+def test_pack_sweep(dev, seed):
+    """Codes equal the oracle's (code/lema/attention.py:82-97), with -0, NaN and the infinities
+    among the values."""
+    from latest_exact_match_attention_amd import pack_codes
+    case = draw_pack_case(9000 + seed)
+    print("case", case, flush=True)
+    B, H, T, D = case["B"], case["H"], case["T"], case["D"]
+    gen = torch.Generator(device="cpu").manual_seed(case["seed"])
+    tdt = TORCH[case["dtype"]]
+    if case["layout"] == "projection":
+        base = torch.randn(B, T, H * D, generator=gen).to(tdt)
+        view = lambda t: t.view(B, T, H, D).transpose(1, 2)
+    else:
+        base = torch.randn(B, H, T, D, generator=gen).to(tdt)
+        view = lambda t: t
+    flat = base.view(-1)
+    n = min(flat.numel(), 5)
+    flat[:n] = torch.tensor([0.0, -0.0, float("nan"), float("inf"), -float("inf")])[:n].to(tdt)
+    zc = view(base).contiguous()
+    carrier = zc.numpy() if case["dtype"] == "f32" else zc.view(torch.int16).numpy().view(np.uint16)
+    want = oracle.pack_codes(carrier, case["dtype"])
+    got = pack_codes(view(base.to(dev)), case["code_dtype"]).cpu().numpy()
+    got = got.view(np.uint32).astype(np.uint64) if case["code_dtype"] == torch.int32 else \
+        got.view(np.uint64)
+    assert np.array_equal(got, want)
+
+
+def test_pack_sweep_covers_the_paths():
+    """Both tile sizes of the 64-head projection view, the dense and the generic layouts, all
+    three dtypes and both code widths."""
+    cases = [draw_pack_case(9000 + s) for s in range(32)]
+    proj64 = [c for c in cases if c["layout"] == "projection" and c["H"] == 64]
+    assert any(c["B"] * c["H"] * c["T"] >= 1 << 21 for c in proj64)
+    assert any(c["B"] * c["H"] * c["T"] < 1 << 21 for c in proj64)
+    assert any(c["layout"] == "contiguous" for c in cases)
+    assert {c["dtype"] for c in cases} == {"f32", "bf16", "f16"}
+    assert {c["code_dtype"] for c in cases} == {torch.int32, torch.int64}
