@@ -12,7 +12,11 @@ d_v]) and the miss fill. Indices and value bits must equal the oracle's
 Store: each case draws partitions, a sequence of exchanges over group ranges (decode-sized,
 chunked and bulk calls, some insert-only), code width and alphabet with codes 0 and all-ones,
 value row width and the final load; outputs, counts and table content must equal one dict per
-partition (code/tests/test_store.py:17-41)."""
+partition (code/tests/test_store.py:17-41).
+
+Model: small LEMA models of random geometry (code widths up to 64 bits) in fp32 or bf16; the
+loss must equal the functional oracle model's and every layer's exact op the sort-based
+algorithm's."""
 import numpy as np
 import pytest
 import torch
@@ -279,3 +283,56 @@ def test_pack_sweep_covers_the_paths():
     assert any(c["layout"] == "contiguous" for c in cases)
     assert {c["dtype"] for c in cases} == {"f32", "bf16", "f16"}
     assert {c["code_dtype"] for c in cases} == {torch.int32, torch.int64}
+
+
+# --------------------------------------------------------------------------------- model
+def draw_model_case(seed: int) -> dict:
+    """A small LEMA model: vocabulary, depth, width, heads, code width (up to 64 bits), value
+    width, dtype and a token batch."""
+    rng = np.random.default_rng(seed)
+    heads = int(rng.choice([1, 2, 4, 8]))
+    return {"seed": seed,
+            "geo": dict(vocab_size=int(rng.choice([64, 200, 512])), depth=int(rng.integers(1, 4)),
+                        dim=int(rng.choice([64, 128, 256])), num_heads=heads,
+                        d_qk=int(rng.choice([4, 16, 24, 32, 40, 64])),
+                        d_v=int(rng.choice([8, 16, 24, 48]))),
+            "dtype": str(rng.choice(["f32", "bf16"])),
+            "B": int(rng.integers(1, 3)), "T": int(rng.choice([64, 300, 1025, 2049]))}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(16))
+def test_model_sweep(dev, seed):
+    """The model's loss against the functional oracle model on the same weights and tokens
+    (code/lema/model.py:143-363; within 1e-2 relative in bf16, 1e-4 in fp32), and every layer's
+    exact op, on that layer's own input, bit-exact against the reference's sort-based algorithm
+    (code/lema/attention.py:100-132)."""
+    from oracle import torch_model
+    from oracle.torch_port import latest_prev_match_sorted
+    from latest_exact_match_attention_amd import lema_from_codes, pack_codes
+    from latest_exact_match_attention_amd.model import ModelConfig, Transformer, lm_loss
+    case = draw_model_case(7000 + seed)
+    print("case", case, flush=True)
+    cfg = ModelConfig(**case["geo"])
+    torch.manual_seed(case["seed"])
+    with torch.device(dev):
+        m = Transformer(cfg)
+    m = m.to(TORCH[case["dtype"]]).eval().requires_grad_(False)
+    m.set_hard(True)
+    g = torch.Generator().manual_seed(case["seed"])
+    tok = torch.randint(0, case["geo"]["vocab_size"], (case["B"], case["T"] + 1), generator=g).to(dev)
+    x, y = tok[:, :-1], tok[:, 1:]
+    B, T = x.shape
+    with torch.no_grad():
+        ours = lm_loss(m, x, y, chunk=256).item()
+        want = torch_model.loss(m.state_dict(), cfg, x, y, chunk=256).item()
+        tol = 1e-2 if case["dtype"] == "bf16" else 1e-4
+        assert abs(ours - want) <= tol * abs(want), (ours, want)
+        h = m.tok_emb(x)
+        for i, blk in enumerate(m.blocks):
+            zq, zk, v = blk.attn.project(blk.pre_attn(h))
+            qc, kc = pack_codes(zq), pack_codes(zk)
+            _, src = lema_from_codes(qc, kc, v, return_src=True)
+            ref = latest_prev_match_sorted(qc.reshape(-1, T), kc.reshape(-1, T))
+            assert torch.equal(src.long().reshape(-1, T), ref), i
+            h = blk(h)
