@@ -236,6 +236,17 @@ int lema_skinny_norm_swiglu_bf16(const void* x, const void* d, const void* nw, f
                                  void* x_out, const void* wg, const void* wu, int64_t ldw,
                                  int64_t M, int64_t N, int64_t K, void* out, void* stream);
 
+/* The attention input of a decode step and its q, k and v projections in one launch
+ * (code/lema/model.py:224-227, 168-175): h = bf16(x * rsqrt(mean(x^2) + eps) * nw) rounded
+ * exactly as lema_rmsnorm_bf16 rounds it, then lema_skinny_qkv_bf16 of h (rows of K). x:
+ * [M, K] bf16 rows, 16-byte aligned; M <= 32, K <= 2048, and M * (K + 8) * 2 bytes plus the
+ * partial sums within a workgroup's 160 KB of LDS. Replaces norm1 + project + pack_codes. */
+int lema_skinny_norm_qkv_bf16(const void* x, const void* nw, float eps, const void* wq,
+                              const void* wk, const void* wv, int64_t ldw, int64_t M,
+                              int64_t Nqk, int64_t Nv, int64_t K, int32_t d, int64_t T,
+                              void* qcodes, void* kcodes, int32_t code_bytes, void* v,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

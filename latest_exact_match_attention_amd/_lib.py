@@ -63,6 +63,8 @@ PROTOTYPES = {
     "lema_skinny_swiglu_bf16": ([_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _p], ctypes.c_int),
     "lema_skinny_norm_swiglu_bf16": ([_p, _p, _p, ctypes.c_float, _p, _p, _p, _i64, _i64, _i64,
                                       _i64, _p, _p], ctypes.c_int),
+    "lema_skinny_norm_qkv_bf16": ([_p, _p, ctypes.c_float, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                   _i64, _i32, _i64, _p, _p, _i32, _p, _p], ctypes.c_int),
     "lema_store_exchange_noalloc": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p,
                                      _p, _p], ctypes.c_int),
     "lema_store_exchange_ws": ([_p, _i64, _i64, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _p, _p,

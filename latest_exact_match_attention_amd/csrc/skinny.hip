@@ -19,7 +19,9 @@
 // A swiglu launch can also take the MLP's pre-norm (Block.forward's norm2 with the attention's
 // residual add, code/lema/model.py:229-232): every block then forms the normalised rows
 // itself, with the stand-alone norm kernel's arithmetic (norm_row.h), into LDS and multiplies
-// those; block 0 also writes x + d, the MLP's residual. That saves the norm's launch.
+// those; block 0 also writes x + d, the MLP's residual. That saves the norm's launch. A q/k/v
+// launch takes the attention's pre-norm the same way (norm1, no addend): batch-16 decode steps
+// of the 24-layer LM went 1.428 -> 1.391 ms.
 //
 // Operand layout of v_mfma_f32_16x16x32_bf16 (checked on the device): lane l holds A row l%16
 // and B column l%16, k = 8 * (l / 16) + j, j < 8; the result's register r of lane l is row
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kSkThreads) void skinny_kernel(SkinnyArgs a) {
         const int64_t mr = m + r * kSkWaves < a.M ? m + r * kSkWaves : m;
         xr[r] = a.x + mr * a.ldx;
         dr[r] = a.nd != nullptr ? a.nd + mr * a.K : nullptr;
-        sr[r] = blockIdx.x == 0 ? a.ns + mr * a.K : nullptr;
+        sr[r] = blockIdx.x == 0 && a.ns != nullptr ? a.ns + mr * a.K : nullptr;
       }
       norm_rows<2, kSkNormSteps>(xr, dr, n, a.nw, a.eps, a.K, l, sr, [&](int r, int e, u32x4 h) {
         *reinterpret_cast<u32x4*>(xs + (m + r * kSkWaves) * xst + e) = h;
@@ -406,11 +408,13 @@ extern "C" int lema_skinny_pack_bf16(const void* x, int64_t ldx, const void* w, 
   return launch_ct(a, ct, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, const void* wk,
-                                    const void* wv, int64_t ldw, int64_t M, int64_t Nqk,
-                                    int64_t Nv, int64_t K, int32_t d, int64_t T, void* qcodes,
-                                    void* kcodes, int32_t code_bytes, void* v, void* stream) {
-  clear_error();
+namespace lema {
+namespace {
+
+// The checks and the three segments of a q/k/v launch; `ct` receives its block width.
+int qkv_args(SkinnyArgs& a, int& ct, const void* x, int64_t ldx, const void* wq, const void* wk,
+             const void* wv, int64_t ldw, int64_t M, int64_t Nqk, int64_t Nv, int64_t K,
+             int32_t d, int64_t T, void* qcodes, void* kcodes, int32_t code_bytes, void* v) {
   if (int rc = check_skinny(x, ldx, ldw, M, K)) return rc;
   if (int rc = check_weight(wq, Nqk)) return rc;
   if (int rc = check_weight(wk, Nqk)) return rc;
@@ -423,9 +427,8 @@ extern "C" int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, 
                (long long)T);
   LEMA_REQUIRE(qcodes && kcodes && aligned(qcodes, code_bytes) && aligned(kcodes, code_bytes) &&
                    v != nullptr, "bad output pointer");
-  const int ct = pack_ct(d);
+  ct = pack_ct(d);
   LEMA_REQUIRE(ct > 0, "head width %d does not tile 16..64 columns", d);
-  SkinnyArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.ldx = ldx;
   a.ldw = ldw;
@@ -440,6 +443,53 @@ extern "C" int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, 
                        static_cast<int32_t>(Nqk), kSkPack, 0, code_bytes};
   a.seg[2] = SkSegment{static_cast<const uint16_t*>(wv), nullptr, v, nullptr, Nv,
                        static_cast<int32_t>(Nv), kSkPlain, 0, 0};
+  return LEMA_OK;
+}
+
+}  // namespace
+}  // namespace lema
+
+extern "C" int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, const void* wk,
+                                    const void* wv, int64_t ldw, int64_t M, int64_t Nqk,
+                                    int64_t Nv, int64_t K, int32_t d, int64_t T, void* qcodes,
+                                    void* kcodes, int32_t code_bytes, void* v, void* stream) {
+  clear_error();
+  SkinnyArgs a{};
+  int ct = 0;
+  if (int rc = qkv_args(a, ct, x, ldx, wq, wk, wv, ldw, M, Nqk, Nv, K, d, T, qcodes, kcodes,
+                        code_bytes, v))
+    return rc;
+  return launch_ct(a, ct, static_cast<hipStream_t>(stream));
+}
+
+// The attention's pre-norm inside the q/k/v launch (Block.gpu_pre: norm1, then the
+// projections, code/lema/model.py:224-227): every block normalises the rows of x (contiguous,
+// K elements) into LDS with the stand-alone norm kernel's arithmetic and multiplies those, so
+// the codes and v equal lema_rmsnorm_bf16 followed by lema_skinny_qkv_bf16 with one launch
+// fewer.
+extern "C" int lema_skinny_norm_qkv_bf16(const void* x, const void* nw, float eps,
+                                         const void* wq, const void* wk, const void* wv,
+                                         int64_t ldw, int64_t M, int64_t Nqk, int64_t Nv,
+                                         int64_t K, int32_t d, int64_t T, void* qcodes,
+                                         void* kcodes, int32_t code_bytes, void* v,
+                                         void* stream) {
+  clear_error();
+  SkinnyArgs a{};
+  int ct = 0;
+  if (int rc = qkv_args(a, ct, x, K, wq, wk, wv, ldw, M, Nqk, Nv, K, d, T, qcodes, kcodes,
+                        code_bytes, v))
+    return rc;
+  LEMA_REQUIRE(K <= 512 * kSkNormSteps, "the fused norm takes rows of at most %d elements, got K=%lld",
+               512 * kSkNormSteps, (long long)K);
+  // LDS: the rows (M x (K + 8) bf16) next to the partial sums (8 x 16 or 32 rows x 16 ct + 1)
+  const int64_t lds = M * (K + 8) * 2 + kSkWaves * (M <= 16 ? 16 : 32) * (16 * ct + 1) * 4;
+  LEMA_REQUIRE(lds <= 160 * 1024, "%lld rows of %lld do not fit the LDS of a workgroup",
+               (long long)M, (long long)K);
+  LEMA_REQUIRE(nw != nullptr && aligned(nw, 16), "norm weight must be a 16-byte aligned device pointer");
+  a.nd = nullptr;
+  a.nw = static_cast<const uint16_t*>(nw);
+  a.ns = nullptr;
+  a.eps = eps;
   return launch_ct(a, ct, static_cast<hipStream_t>(stream));
 }
 

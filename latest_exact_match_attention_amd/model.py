@@ -157,10 +157,13 @@ def _pack_tiles(d: int) -> bool:
     return d % 8 == 0 or any((16 * c) % d == 0 for c in (1, 2, 3, 4))
 
 
-def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype):
+def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype, norm: nn.RMSNorm | None = None):
     """[B, T, dim] -> (qc, kc [B, H, T] codes, v [B, H, T, d_v] view) with all three
     projections in one launch (skinny MFMA kernel, pack epilogues for q and k), or None when
-    the shape is not decode-sized or the heads differ in count."""
+    the shape is not decode-sized or the heads differ in count. With `norm`, x is the layer's
+    input and the launch normalises it first, rounded as rms_norm rounds it (the same codes and
+    v as rms_norm followed by this, with one launch fewer); None also where that does not
+    apply."""
     c = at.cfg
     wq, wk, wv = at.q_proj.weight, at.k_proj.weight, at.v_proj.weight
     if not (_skinny(x, wq) and x.dim() == 3 and wq.shape == wk.shape and _pack_tiles(c.d_qk)
@@ -169,13 +172,27 @@ def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype):
         return None
     B, T, K = x.shape
     Nqk, Nv = wq.shape[0], wv.shape[0]
+    if norm is not None:
+        M = B * T
+        ct = 1 if c.d_qk % 8 == 0 else next(k for k in range(1, 5) if (16 * k) % c.d_qk == 0)
+        if not (_fused(norm.weight) and norm.weight.data_ptr() % 16 == 0 and x.is_contiguous()
+                and K <= 2048
+                and M * (K + 8) * 2 + 8 * (16 if M <= 16 else 32) * (16 * ct + 1) * 4 <= 160 * 1024):
+            return None
     qc = torch.empty((B, Nqk // c.d_qk, T), dtype=code_dtype, device=x.device)
     kc = torch.empty_like(qc)
     v = torch.empty((B, T, Nv), dtype=x.dtype, device=x.device)
-    _lib.check(_lib.lib().lema_skinny_qkv_bf16(
-        x.data_ptr(), K, wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), K, B * T, Nqk, Nv, K,
-        c.d_qk, T, qc.data_ptr(), kc.data_ptr(), qc.element_size(), v.data_ptr(),
-        _lib.stream_of(x)))
+    if norm is not None:
+        eps = norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
+        _lib.check(_lib.lib().lema_skinny_norm_qkv_bf16(
+            x.data_ptr(), norm.weight.data_ptr(), float(eps), wq.data_ptr(), wk.data_ptr(),
+            wv.data_ptr(), K, B * T, Nqk, Nv, K, c.d_qk, T, qc.data_ptr(), kc.data_ptr(),
+            qc.element_size(), v.data_ptr(), _lib.stream_of(x)))
+    else:
+        _lib.check(_lib.lib().lema_skinny_qkv_bf16(
+            x.data_ptr(), K, wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), K, B * T, Nqk, Nv, K,
+            c.d_qk, T, qc.data_ptr(), kc.data_ptr(), qc.element_size(), v.data_ptr(),
+            _lib.stream_of(x)))
     return qc, kc, v.view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
 
 
@@ -360,11 +377,14 @@ class Block(nn.Module):
 
     def gpu_pre(self, x):
         """Normalise, project, pack both codes (code/lema/model.py:224-227). On decode shapes
-        the three projections are one launch, q and k going straight to codes (skinny MFMA
-        kernel, pack epilogues)."""
-        h = self.pre_attn(x)
+        the norm and the three projections are one launch, q and k going straight to codes
+        (skinny MFMA kernel: pre-norm prologue, pack epilogues)."""
         at, c = self.attn, self.attn.cfg
         ct = code_dtype_for(c.d_qk)
+        fused = project_qkv(x, at, ct, norm=self.norm1)
+        if fused is not None:
+            return fused
+        h = self.pre_attn(x)
         fused = project_qkv(h, at, ct)
         if fused is not None:
             return fused

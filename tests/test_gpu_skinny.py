@@ -188,3 +188,66 @@ def test_block_mlp_half_fused_equals_unfused(dev, B):
         want = mlp(h, residual=s)
     assert got is not None
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 32])
+@pytest.mark.parametrize("K,d,H", [(1536, 24, 64), (256, 16, 8), (2048, 64, 16), (2048, 12, 8),
+                                   (64, 40, 2)])
+def test_skinny_norm_qkv_equals_unfused(dev, M, K, d, H):
+    """The attention's pre-norm inside the q/k/v launch against the norm kernel followed by the
+    q/k/v launch, codes and v bit for bit. Rows that do not fit a workgroup's LDS beside the
+    partial sums (32 rows of 2048 with 48-column blocks) are refused on the host."""
+    from latest_exact_match_attention_amd.model import rms_norm
+    g = torch.Generator(device=dev).manual_seed(M * 5 + K + d)
+    T = 1 if M % 2 else 2
+    B = M // T
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    norm = torch.nn.RMSNorm(K, eps=1e-5).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(K, device=dev, generator=g))
+    wq, wk = ((torch.randn(H * d, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+              for _ in range(2))
+    Nv = H * 24
+    wv = (torch.randn(Nv, K, device=dev, generator=g) / K ** 0.5).to(torch.bfloat16)
+    ct = torch.int32 if d <= 32 else torch.int64
+    qc = torch.full((B, H, T), -1, dtype=ct, device=dev)
+    kc = torch.full_like(qc, -1)
+    v = torch.empty((M, Nv), dtype=torch.bfloat16, device=dev)
+    args = (x.data_ptr(), norm.weight.data_ptr(), 1e-5, wq.data_ptr(), wk.data_ptr(),
+            wv.data_ptr(), K, M, H * d, Nv, K, d, T, qc.data_ptr(), kc.data_ptr(),
+            qc.element_size(), v.data_ptr(), _lib.stream_of(x))
+    blocks = 1 if d % 8 == 0 else next(c for c in (1, 2, 3, 4) if (16 * c) % d == 0)
+    if M * (K + 8) * 2 + 8 * (16 if M <= 16 else 32) * (16 * blocks + 1) * 4 > 160 * 1024:
+        with pytest.raises(Exception, match="LDS"):
+            _lib.check(_lib.lib().lema_skinny_norm_qkv_bf16(*args))
+        return
+    _lib.check(_lib.lib().lema_skinny_norm_qkv_bf16(*args))
+    with torch.no_grad():
+        h, _ = rms_norm(x, norm)
+    wq_, wk_ = torch.full_like(qc, -1), torch.full_like(kc, -1)
+    wv_ = torch.empty_like(v)
+    _lib.check(_lib.lib().lema_skinny_qkv_bf16(
+        h.data_ptr(), K, wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), K, M, H * d, Nv, K, d, T,
+        wq_.data_ptr(), wk_.data_ptr(), wq_.element_size(), wv_.data_ptr(), _lib.stream_of(x)))
+    assert torch.equal(qc, wq_) and torch.equal(kc, wk_)
+    assert torch.equal(v.view(torch.int16), wv_.view(torch.int16))
+
+
+@pytest.mark.parametrize("B", [1, 16])
+def test_block_attention_input_fused_equals_unfused(dev, B):
+    """Block.gpu_pre on a decode step (norm1 inside the q/k/v launch) returns the codes and v
+    that rms_norm followed by the q/k/v launch returns, bit for bit."""
+    from latest_exact_match_attention_amd.model import Block, ModelConfig, project_qkv
+    from latest_exact_match_attention_amd.attention import code_dtype_for
+    torch.manual_seed(B)
+    cfg = ModelConfig(vocab_size=256, depth=1, dim=1536, num_heads=64)
+    blk = Block(cfg).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        blk.norm1.weight.copy_(1 + 0.1 * torch.randn(1536, device=dev))
+    x = torch.randn(B, 1, 1536, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        qc, kc, v = blk.gpu_pre(x)
+        want = project_qkv(blk.pre_attn(x), blk.attn, code_dtype_for(cfg.d_qk))
+    assert want is not None
+    assert torch.equal(qc, want[0]) and torch.equal(kc, want[1])
+    assert torch.equal(v.view(torch.int16), want[2].view(torch.int16))
