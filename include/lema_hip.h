@@ -141,8 +141,10 @@ int lema_store_exchange_ws(void* table, int64_t cap, int64_t vbytes, const void*
 
 /* lema_store_exchange with no workspace argument that allocates nothing: a call that takes
  * the bulk path (as lema_store_workspace_bytes would report) runs on a scratch array inside
- * the library, LEMA_NOALLOC_SCRATCH_BYTES per GPU, held from the first such call on that GPU
- * until the process ends, in consecutive slices of its partitions sized to fit it. Same
+ * the library, LEMA_NOALLOC_SCRATCH_BYTES per GPU, in consecutive slices of its partitions
+ * sized to fit it. The array is part of the library's code object: it is reserved on every GPU
+ * where the library's kernels are loaded, whether or not this entry point is ever called, and
+ * lasts for the life of the process. Same
  * results as lema_store_exchange_ws. No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops). Make the first
  * call on a device outside graph capture (it looks the scratch's address up). Calls that

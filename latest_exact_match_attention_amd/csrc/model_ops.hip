@@ -116,7 +116,9 @@ __global__ __launch_bounds__(256) void xent_kernel(const uint16_t* logits, int64
     for (int k = 0; k < 8; ++k) sa += __builtin_amdgcn_exp2f(fmaf(x[k], kLog2e, -mb));
 #pragma unroll
     for (int k = 8; k < 16; ++k) sb += __builtin_amdgcn_exp2f(fmaf(x[k], kLog2e, -mb));
-    s += two ? sa + sb : sa;
+    // while every logit so far is -inf, m is -inf and each term is exp2(-inf + inf) = NaN:
+    // such a trip adds nothing (e^-inf = 0), as in the combine below
+    if (m != -INFINITY) s += two ? sa + sb : sa;
   }
   // combine: wavefront, then the 4 wavefronts
 #pragma unroll

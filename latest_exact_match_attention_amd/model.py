@@ -17,8 +17,11 @@ same weights.
 In bf16 on the GPU the SwiGLU product, both pre-norms (the MLP's with the attention residual
 add), the final norm and the loss run as fused HIP kernels (the reference compiles these
 segments with torch.compile). The norm kernel rounds like torch's RMSNorm (one rounding of
-x * rstd * w from fp32), so the codes, the signs of the attention input's projections, stay
-the ones torch's norm gives.
+x * rstd * w from fp32) but adds up the mean of squares in its own order, so a rare element
+of the attention input lands one bf16 ulp from torch's. The codes, the signs of that input's
+projections, can then differ from the ones torch's norm gives, only at pre-activations
+within 1e-3 of zero (the stated binarization tolerance; at the full LM shape 9 of 1e8 code
+bits of the first layer).
 
 Only the hard (exact) op is implemented: the training surrogate (stick-breaking relaxation,
 straight-through binarization) and the softmax / gated-deltanet baselines are not part of the
@@ -29,6 +32,7 @@ from __future__ import annotations
 import dataclasses
 import math
 from dataclasses import dataclass
+from pathlib import Path
 
 import torch
 import torch.nn.functional as F
@@ -38,7 +42,7 @@ from . import _lib
 from .attention import code_dtype_for, lema_hard, pack_codes
 
 __all__ = ["ModelConfig", "SwiGLU", "Attention", "Block", "Transformer", "lm_loss", "rms_norm",
-           "embed", "argmax_into",
+           "embed", "argmax_into", "load_trained",
            "swiglu", "cross_entropy_sum"]
 
 # ------------------------------------------------------------------ fused bf16 segments
@@ -219,8 +223,6 @@ class ModelConfig:
     num_kv_heads: int = 0
     attn: str = "lema"
     pos: str = "nope"
-    rope_base: float = 10000.0
-    gdn_expand_v: int = 2
     norm_eps: float = 1e-5
 
     def __post_init__(self):
@@ -330,14 +332,11 @@ class Attention(nn.Module):
         super().__init__()
         self.cfg = cfg
         self.kind = cfg.attn
-        self.inner = None
         self.q_proj = nn.Linear(cfg.dim, cfg.num_heads * cfg.d_qk, bias=False)
         self.k_proj = nn.Linear(cfg.dim, cfg.num_kv_heads * cfg.d_qk, bias=False)
         self.v_proj = nn.Linear(cfg.dim, cfg.num_kv_heads * cfg.d_v, bias=False)
         self.o_proj = nn.Linear(cfg.num_heads * cfg.d_v, cfg.dim, bias=False)
-        self.alpha, self.cap, self.c, self.beta = 1.0, 2.0, 0.0, 2.0
         self.hard = False
-        self.exact_fwd = False
 
     def project(self, x):
         """`[B, T, dim]` -> query and key pre-activations and values, `[B, H, T, d]`."""
@@ -506,3 +505,27 @@ def lm_loss(model: Transformer, x: torch.Tensor, y: torch.Tensor, chunk: int = 1
         hc = h[:, a:a + chunk].reshape(-1, h.shape[-1]).contiguous()
         total += cross_entropy_sum(model.lm_head(hc), y[:, a:a + chunk].reshape(-1))
     return total / y.numel()
+
+
+def load_trained(path, device="cuda") -> tuple[Transformer, ModelConfig]:
+    """A finished training run, ready to evaluate (code/lema/model.py:420-436): `path` is the
+    run directory (its `model.pt`) or a checkpoint file, a dict holding `config` (the
+    ModelConfig fields) and `state_dict`. The model comes back in hard mode, fp32, in eval
+    mode; parameters the checkpoint holds beyond this model's are dropped.
+
+    The file is read with `torch.load(weights_only=True)`, which builds tensors and plain
+    containers only and executes nothing from the file; a checkpoint that needs arbitrary
+    objects to load raises instead. Only all-LEMA configurations load (ModelConfig raises
+    ValueError for the others)."""
+    path = Path(path)
+    if path.is_dir():
+        path = path / "model.pt"
+    ck = torch.load(path, map_location="cpu", weights_only=True)
+    if not isinstance(ck, dict) or "config" not in ck or "state_dict" not in ck:
+        raise ValueError(f"{path}: expected a dict with 'config' and 'state_dict'")
+    cfg = ModelConfig.from_dict(dict(ck["config"]))
+    model = Transformer(cfg).to(device).eval()
+    keep = model.state_dict().keys()
+    model.load_state_dict({k: v for k, v in ck["state_dict"].items() if k in keep})
+    model.set_hard(True)
+    return model, cfg

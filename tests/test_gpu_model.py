@@ -101,9 +101,14 @@ def test_bf16_token_steps_match_oracle_loss(dev, heads):
 
 def check_layers(m, cfg, x, sd):
     """Every layer: the exact op on the model's own codes equals the reference's sort-based
-    algorithm on them, bit for bit. Layer 0's codes equal the functional oracle's exactly: the
-    product's attention pre-norm (the fused norm kernel in bf16) gives torch's RMSNorm output,
-    and the projections are the same torch GEMMs on the same embedding."""
+    algorithm on them, bit for bit.
+
+    Layer 0 against the functional oracle (torch's RMSNorm, then torch's bf16 GEMMs on the same
+    embedding): the product's attention pre-norm is the fused norm kernel, which rounds like
+    torch's RMSNorm but sums the mean of squares in another order, so an element can land one
+    bf16 ulp apart. The stated binarization tolerance then bounds what may differ: a query or
+    key code bit only where its pre-activation is within 1e-3 of zero, at most 1e-5 of all
+    code bits, and at most 1e-4 of the match indices against the oracle's own codes."""
     from oracle.torch_port import latest_prev_match_sorted
     from latest_exact_match_attention_amd import lema_from_codes, pack_codes
     B, T = x.shape
@@ -118,17 +123,25 @@ def check_layers(m, cfg, x, sd):
         if i == 0:
             hz = torch.nn.functional.rms_norm(h, (cfg.dim,), sd["blocks.0.norm1.weight"],
                                               cfg.norm_eps)
-            zo = torch.nn.functional.linear(hz, sd["blocks.0.attn.q_proj.weight"])
-            zo = zo.view(B, T, cfg.num_heads, cfg.d_qk).transpose(1, 2)
-            diff = (qc.long() & 0xFFFFFFFF) ^ torch_model.pack(zo)
-            # The stated binarization tolerance: a code bit may differ from the oracle's only
-            # where its pre-activation is within 1e-3 of zero (the two norms add up the mean of
-            # squares in different orders, so a rare element lands one bf16 ulp apart).
-            bits = (diff.unsqueeze(-1) >> torch.arange(cfg.d_qk, device=diff.device)) & 1
-            flipped = bits.bool()
-            assert (zo.float().abs()[flipped] < 1e-3).all(), zo.float().abs()[flipped].max()
-            print(f"layer 0: {int(flipped.sum())} of {flipped.numel()} code bits differ from "
-                  f"the oracle's, all at |z| < 1e-3", flush=True)
+            flips, nbits, ocodes = 0, 0, []
+            for ours, w in ((qc, "q_proj"), (kc, "k_proj")):
+                zo = torch.nn.functional.linear(hz, sd[f"blocks.0.attn.{w}.weight"])
+                zo = zo.view(B, T, cfg.num_heads, cfg.d_qk).transpose(1, 2)
+                oc = torch_model.pack(zo)
+                ocodes.append(oc)
+                diff = (ours.long() & 0xFFFFFFFF) ^ oc
+                bits = (diff.unsqueeze(-1) >> torch.arange(cfg.d_qk, device=diff.device)) & 1
+                flipped = bits.bool()
+                assert (zo.float().abs()[flipped] < 1e-3).all(), (w, zo.float().abs()[flipped].max())
+                flips += int(flipped.sum())
+                nbits += flipped.numel()
+            assert flips <= 1e-5 * nbits, (flips, nbits)
+            osrc = latest_prev_match_sorted(ocodes[0].reshape(-1, T), ocodes[1].reshape(-1, T))
+            moved = int((osrc != want).sum())
+            assert moved <= 1e-4 * want.numel(), (moved, want.numel())
+            print(f"layer 0: {flips} of {nbits} query and key code bits differ from the "
+                  f"oracle's, all at |z| < 1e-3; {moved} of {want.numel()} match indices "
+                  f"differ from the oracle's", flush=True)
         h = blk(h)
 
 

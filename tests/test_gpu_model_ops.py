@@ -62,7 +62,8 @@ def test_cross_entropy_rows(dev, V, scale):
     """Every row's loss within 1e-6 of an fp32 cross-entropy, relative to the loss or to 1
     where the loss is smaller (float32 rounding of log S + M - x_t): vocabularies that end
     inside a thread's first or second piece, logits spread from 1 to 30 standard deviations,
-    and -inf logits (a masked entry adds nothing)."""
+    and -inf logits (a masked entry adds nothing, also where a thread's first pieces are
+    wholly masked)."""
     from latest_exact_match_attention_amd import _lib
     g = torch.Generator(device=dev).manual_seed(V)
     rows = 37
@@ -71,6 +72,10 @@ def test_cross_entropy_rows(dev, V, scale):
     logits[1, (y[1] + 1) % V] = -float("inf")
     logits[2, :: 3] = -float("inf")
     logits[2, y[2]] = 0.5
+    # a contiguous masked block: every logit of some threads' first trips (and, past 4096,
+    # whole trips) is -inf
+    logits[3, : min(V - 1, 4096 + 8)] = -float("inf")
+    logits[3, y[3]] = 1.25
     loss = torch.empty(rows, device=dev, dtype=torch.float32)
     _lib.check(_lib.lib().lema_cross_entropy_bf16(logits.data_ptr(), rows, V, V, y.data_ptr(),
                                                   loss.data_ptr(), _lib.stream_of(logits)))

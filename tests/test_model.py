@@ -205,3 +205,28 @@ def test_forward_and_decode_step_issue_no_batched_products(monkeypatch):
         ops = _aten_ops(step)
         assert "aten::bmm" not in ops, sorted(ops)
         assert cache.t == 48 + 1
+
+
+def test_load_trained_reads_a_run_directory(tmp_path):
+    """load_trained (code/lema/model.py:420-436): a run directory's model.pt with the config
+    as a plain dict (reference-only fields among them) and a state dict holding one entry this
+    model does not have; the model comes back with those weights, in hard mode."""
+    import dataclasses
+    from latest_exact_match_attention_amd.model import load_trained
+    cfg = ModelConfig(vocab_size=300, depth=2, dim=64, num_heads=4, d_qk=8, d_v=16)
+    torch.manual_seed(3)
+    src = Transformer(cfg)
+    conf = dataclasses.asdict(cfg) | {"rope_base": 10000.0, "gdn_expand_v": 2}
+    sd = dict(src.state_dict()) | {"blocks.0.attn.inner.extra": torch.zeros(3)}
+    torch.save({"config": conf, "state_dict": sd, "step": 7}, tmp_path / "model.pt")
+    torch.manual_seed(4)                      # a different draw: the weights must come from disk
+    m, c = load_trained(tmp_path, device="cpu")
+    assert c == cfg and not m.training and all(a.hard for a in m.lema_layers())
+    for k, v in src.state_dict().items():
+        assert torch.equal(m.state_dict()[k], v), k
+    # a checkpoint that needs an arbitrary object to load is refused, not executed
+    import fractions
+    torch.save({"config": conf, "state_dict": sd, "obj": fractions.Fraction(1, 3)},
+               tmp_path / "bad.pt")
+    with pytest.raises(Exception, match="[Ww]eights only"):
+        load_trained(tmp_path / "bad.pt", device="cpu")

@@ -82,3 +82,75 @@ def test_noalloc_insert_only_and_errors(dev):
                                        a.counts_device.data_ptr(), a.full_flag.data_ptr(),
                                        _lib.stream_of(kc))
     assert rc == _lib.BAD_ARG and b"partitions x T" in L.lema_last_error()
+
+
+def test_noalloc_replays_in_a_graph(dev):
+    """The entry point under HIP graph capture, its intended use: after one eager call (which
+    looks the scratch address up), a long call spanning several scratch slices and a decode
+    step are captured on one stream. Replayed twice, each time with fresh codes and values
+    written into the captured inputs, every output, the counts and the table's entries equal
+    the same calls on a twin store through lema_store_exchange_ws."""
+    rng = np.random.default_rng(11)
+    groups, cap = 64, 9_000_000
+    a = HashStore(D_V, groups=groups, dtype=torch.bfloat16, capacity=cap, device=dev)
+    b = HashStore(D_V, groups=groups, dtype=torch.bfloat16, capacity=cap, device=dev)
+    P, T = 64, 40_000
+    assert _lib.lib().lema_store_workspace_bytes(P * T, T, 4) > _lib.NOALLOC_SCRATCH_BYTES
+
+    def draw(n, spread):
+        c = rng.integers(0, spread, n)
+        c[::5] = rng.integers(0, 2**31, c[::5].size)
+        return torch.from_numpy(c).to(dev).to(torch.int32)
+
+    bufs = {"long": (P * T, T), "step": (P, 1)}
+    ins = {k: [torch.empty(n, dtype=torch.int32, device=dev),
+               torch.empty(n, dtype=torch.int32, device=dev),
+               torch.empty((n, D_V), dtype=torch.bfloat16, device=dev),
+               torch.empty((n, D_V), dtype=torch.bfloat16, device=dev)]
+           for k, (n, _) in bufs.items()}
+
+    def refill():
+        for k, (n, _) in bufs.items():
+            q, kk, v, _o = ins[k]
+            q.copy_(draw(n, 40_000))
+            kk.copy_(draw(n, 40_000))
+            v.copy_(torch.randn((n, D_V), device=dev).to(torch.bfloat16))
+
+    def run_b():
+        outs = {}
+        for k, (n, t) in bufs.items():
+            q, kk, v, _o = ins[k]
+            outs[k] = torch.empty((n, D_V), dtype=torch.bfloat16, device=dev)
+            b.exchange(q, kk, v, outs[k], t, 0)
+        return outs
+
+    def compare(outs):
+        for k in bufs:
+            assert torch.equal(ins[k][3].view(torch.int16), outs[k].view(torch.int16)), k
+        assert torch.equal(a.counts, b.counts)
+
+    # eager warm-up on the same buffers, then the capture
+    refill()
+    for k, (n, t) in bufs.items():
+        q, kk, v, o = ins[k]
+        noalloc(a, q, kk, v, o, t, 0)
+    compare(run_b())
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for k, (n, t) in bufs.items():
+                q, kk, v, o = ins[k]
+                noalloc(a, q, kk, v, o, t, 0)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    for rep in range(2):
+        refill()
+        torch.cuda.synchronize(dev)
+        g.replay()
+        torch.cuda.synchronize(dev)
+        a.check_full()
+        compare(run_b())
+    ka, va = entries(a)
+    kb, vb = entries(b)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
