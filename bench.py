@@ -51,7 +51,10 @@ Codes come from a counter-based hash of (seed, head, position) and values from a
 seeded generator, made on the device for each call before it is timed. `value` = queries
 per second over the timed exchanges. The first call also runs through the reference's own
 C++ store on the host (`--long-parity-calls` of them): outputs and counts must agree bit for
-bit, and its time is the CPU baseline.
+bit, and its time is the CPU baseline. Each value row's first 8 bytes name its key (head,
+position + 1); after the timed calls, every query of every call is checked against the
+reference's sort-based algorithm run per head over all positions on the device, and the final
+counts against each head's distinct key codes (`parity.all_calls`; `--no-full-parity` skips it).
 
 decode_model: single-token decoding of the lm_forward model (24 layers, d_model 1536, 64
 heads, bf16) for a batch of 16 streams after a 4,096-token prompt, through the HBM store with
@@ -111,6 +114,9 @@ def parse():
                     help="calls of 2^20 positions of the long_context workload to run")
     ap.add_argument("--long-parity-calls", type=int, default=1,
                     help="leading calls also run through the reference store on the host")
+    ap.add_argument("--no-full-parity", action="store_true",
+                    help="long_context: skip checking every call's outputs against the "
+                         "sort-based oracle after the timed calls")
     ap.add_argument("--lm-batch", type=int, default=4)
     ap.add_argument("--lm-seq", type=int, default=16384)
     ap.add_argument("--lm-cpu-tokens", type=int, default=512,
@@ -705,11 +711,32 @@ def bench_long(a):
         del probe
     total_ms, per_call, cpu_s, same, counts_same = 0.0, [], [], True, True
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # Every value row's first 8 bytes name its key, (head << 32) | (position + 1), so each
+    # returned row says which key it came from (0: a miss); the rows stay opaque to the store.
+    full = not a.no_full_parity
+    if full:
+        qc_all = torch.empty((H, L * calls), dtype=torch.int64, device=dev)
+        kc_all = torch.empty_like(qc_all)
+        got_all = torch.empty_like(qc_all)
+    head = torch.arange(H, dtype=torch.int64, device=dev).view(H, 1)
+    # untimed warm-up: the first call's inputs through a separate store sized for one call,
+    # which loads the kernels and leaves a workspace of the call's size in torch's allocator;
+    # the timed calls then start on the workload's own fresh table
+    wq, wk = long_context_codes(0, H, 0, L, dev)
+    warm = HashStore(dv, groups=H, dtype=torch.bfloat16, capacity=math.ceil(H * L / 0.5),
+                     device=dev)
+    wv = torch.zeros((H * L, dv), dtype=torch.bfloat16, device=dev)
+    warm.exchange(wq.to(torch.int32).view(-1), wk.to(torch.int32).view(-1), wv,
+                  torch.empty_like(wv), L, 0)
+    del warm, wq, wk, wv
+    torch.cuda.synchronize()
     for c in range(calls):
         qc64, kc64 = long_context_codes(0, H, c * L, (c + 1) * L, dev)
         qc, kc = qc64.to(torch.int32).contiguous(), kc64.to(torch.int32).contiguous()
         g = torch.Generator(device=dev).manual_seed(1000 + c)
         v = torch.randn((H * L, dv), device=dev, generator=g).to(torch.bfloat16)
+        pos = torch.arange(c * L, (c + 1) * L, dtype=torch.int64, device=dev).view(1, L)
+        v.view(torch.int64).view(H, L, dv // 4)[:, :, 0] = (head << 32) | (pos + 1)
         out = torch.empty_like(v)
         torch.cuda.synchronize()
         e0.record(stream)
@@ -721,6 +748,10 @@ def bench_long(a):
         total_ms += ms
         per_call.append(round(ms, 3))
         print(f"long_context call {c + 1}/{calls}: {ms:.2f} ms", file=sys.stderr, flush=True)
+        if full:
+            qc_all[:, c * L:(c + 1) * L] = qc64
+            kc_all[:, c * L:(c + 1) * L] = kc64
+            got_all[:, c * L:(c + 1) * L] = out.view(torch.int64).view(H, L, dv // 4)[:, :, 0]
         if c < n_par:
             qh, kh = qc64.view(-1).cpu(), kc64.view(-1).cpu()
             vh = v.view(torch.int16).cpu()
@@ -733,6 +764,29 @@ def bench_long(a):
             print(f"  reference store: {cpu_s[-1]:.2f} s, outputs identical: {same}, "
                   f"counts identical: {counts_same}", file=sys.stderr, flush=True)
         del qc64, kc64, qc, kc, v, out
+    full_par = None
+    if full:
+        # after the timed calls: per head, the reference's sort-based algorithm over every
+        # position of the run (oracle/torch_port.py, on the device) names each query's key
+        from oracle.torch_port import latest_prev_match_sorted
+        bad, hits, counts_ok = 0, 0, True
+        for h in range(H):
+            src = latest_prev_match_sorted(qc_all[h:h + 1], kc_all[h:h + 1])[0]
+            want = torch.where(src >= 0, (h << 32) | (src + 1), torch.zeros_like(src))
+            bad += int((got_all[h] != want).sum())
+            hits += int((src >= 0).sum())
+            counts_ok = counts_ok and int(store.counts[h]) == torch.unique(kc_all[h]).numel()
+        full_par = {"calls_checked": calls, "queries_checked": H * L * calls,
+                    "queries_differing": bad, "counts_equal_distinct_keys": counts_ok,
+                    "hit_rate": round(hits / (H * L * calls), 4),
+                    "oracle": "sort-based latest match over all positions per head "
+                              "(code/lema/attention.py:100-132), on the device"}
+        print(f"long_context: all {calls} calls against the sort-based oracle: {bad} of "
+              f"{H * L * calls} queries differ, counts equal distinct keys: {counts_ok}",
+              file=sys.stderr, flush=True)
+        if bad or not counts_ok:
+            print("long_context full-run parity FAILED", file=sys.stderr)
+        del qc_all, kc_all, got_all
     nq = H * L * calls
     bpq = 4 + 4 + 4 + 2 * 2 * dv
     achieved = bpq * nq / (total_ms * 1e-3) / 1e9
@@ -741,6 +795,8 @@ def bench_long(a):
     if n_par:
         parity = {"calls_checked": n_par, "outputs_identical": same,
                   "counts_identical_after_checked_calls": counts_same}
+    if full_par is not None:
+        parity = dict(parity or {}, reference_store_calls=n_par, all_calls=full_par)
         cpu = {"value": H * L * n_par / sum(cpu_s), "unit": "queries/s", "cores": threads,
                "kind": "reference", "cpu_model": cpu_model(),
                "sample": f"the first {n_par} call(s) of 64 x 2^20 positions through "
@@ -754,13 +810,14 @@ def bench_long(a):
         "unit": "queries/s",
         "n_gpus": 1,
         "steps": calls,
-        "warmup": 0,
+        "warmup": 1,
         "ms_per_step": total_ms / calls,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int32 codes (32-bit), bf16 values (opaque 48-byte rows)",
-        "data": "synthetic (counter-based hash codes, seed 0; per-call seeded N(0,1) values)",
+        "data": "synthetic (counter-based hash codes, seed 0; per-call seeded N(0,1) values, "
+                "each row's first 8 bytes naming its key)",
         "config": {"workload": "long_context", "B": 1, "H": H, "T": L * calls,
                    "positions_per_call": L, "calls": calls, "d_v": dv, "capacity": cap,
                    "table_bytes": cap * (16 + 2 * dv), "load_after": round(store.load(), 4),

@@ -109,3 +109,55 @@ def test_long_context_workload_first_calls(dev, ref):
         assert hits > 0.05
     del store, host
     torch.cuda.empty_cache()
+
+
+def test_long_context_workload_all_calls(dev):
+    """The whole long-context run: all 16 calls of 2^20 positions of the 64 heads through the
+    workload's 137 GB table. Each value row carries its key's own (head, position + 1) in its
+    first 8 bytes (the store copies rows as opaque bytes), so every returned row names the key
+    it came from, and a miss returns 0. Per head, the reference's sort-based algorithm
+    (code/lema/attention.py:100-132, oracle/torch_port.py, on the device) over all 2^24
+    positions gives the latest earlier key with the query's code. Every query of every call
+    must return exactly that key, and the final per-head counts must equal the number of
+    distinct key codes of the head (code/lema/cache.py:27-30: any chunking gives the one-shot
+    result)."""
+    from oracle.torch_port import latest_prev_match_sorted
+    H, T, L, dv = LONG_CONTEXT["H"], LONG_CONTEXT["T"], LONG_CONTEXT["call"], LONG_CONTEXT["dv"]
+    calls = T // L
+    cap = math.ceil(H * T / 0.5)
+    store = HashStore(dv, groups=H, dtype=torch.bfloat16, capacity=cap, device=dev)
+    head = torch.arange(H, dtype=torch.int64, device=dev).view(H, 1)
+    qc_all = torch.empty((H, T), dtype=torch.int64, device=dev)
+    kc_all = torch.empty((H, T), dtype=torch.int64, device=dev)
+    got = torch.empty((H, T), dtype=torch.int64, device=dev)
+    for c in range(calls):
+        t0 = c * L
+        qc64, kc64 = long_context_codes(0, H, t0, t0 + L, dev)
+        qc_all[:, t0:t0 + L] = qc64
+        kc_all[:, t0:t0 + L] = kc64
+        v = torch.zeros((H, L, dv), dtype=torch.int16, device=dev)
+        pos = torch.arange(t0, t0 + L, dtype=torch.int64, device=dev).view(1, L)
+        v.view(torch.int64)[:, :, 0] = (head << 32) | (pos + 1)    # rows: 6 int64 words
+        out = torch.empty((H * L, dv), dtype=torch.bfloat16, device=dev)
+        store.exchange(qc64.to(torch.int32).view(-1), kc64.to(torch.int32).view(-1),
+                       v.view(H * L, dv).view(torch.bfloat16), out, L, 0)
+        got[:, t0:t0 + L] = out.view(torch.int64).view(H, L, dv // 4)[:, :, 0]
+        del v, out
+        say(f"long-context full run: call {c + 1}/{calls} done, table load {store.load():.3f}")
+    assert store.load() > 0.44
+    hits = 0
+    for h in range(H):
+        src = latest_prev_match_sorted(qc_all[h:h + 1], kc_all[h:h + 1])[0]
+        want = torch.where(src >= 0, (h << 32) | (src + 1), torch.zeros_like(src))
+        bad = int((got[h] != want).sum())
+        assert bad == 0, f"head {h}: {bad} of {T} queries differ from the oracle"
+        hits += int((src >= 0).sum())
+        n_keys = torch.unique(kc_all[h]).numel()
+        assert int(store.counts[h]) == n_keys, (h, int(store.counts[h]), n_keys)
+        if h % 16 == 15:
+            say(f"long-context full run: heads 0-{h} equal the oracle over all {calls} calls")
+    say(f"long-context full run: {H * T} queries over {calls} calls identical, hit rate "
+        f"{hits / (H * T):.4f}")
+    assert hits / (H * T) > 0.05
+    del store, qc_all, kc_all, got
+    torch.cuda.empty_cache()
