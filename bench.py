@@ -625,6 +625,20 @@ def bench_lm(a):
         torch.cuda.synchronize()
         ms_l = e0.elapsed_time(e1) / n_l
         ms_lc = cold_ms(lambda: launch_hard(qc, kc, v, yv), stream)
+        # the same op into a head-contiguous y [B, H, T, d_v]: every 128-byte line of y is then
+        # written by one workgroup, where the model's interleaved y (the o_proj input) has each
+        # line assembled in L2 from 48-byte pieces of 8 workgroups
+        yc = torch.empty((B, cfg.num_heads, T, cfg.d_v), dtype=v.dtype, device=dev)
+        launch_hard(qc, kc, v, yc)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n_l):
+            launch_hard(qc, kc, v, yc)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_lcont = e0.elapsed_time(e1) / n_l
+        ms_lcont_cold = cold_ms(lambda: launch_hard(qc, kc, v, yc), stream)
+        del yc
         src = torch.empty((B, cfg.num_heads, T), dtype=torch.int32, device=dev)
         launch_hard(qc, kc, v, yv, src)
         hits = float((src >= 0).float().mean())
@@ -666,7 +680,15 @@ def bench_lm(a):
                         "us": ms_l * 1e3, "queries": nq, "bytes_per_query": bpq,
                         "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS,
                         "us_cold_cache": ms_lc * 1e3,
-                        "frac_cold_cache": bpq * nq / (ms_lc * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                        "frac_cold_cache": bpq * nq / (ms_lc * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                        "y_layout": "interleaved [B, T, H*d_v] (the o_proj input)",
+                        "contiguous_y": {
+                            "y_layout": "head-contiguous [B, H, T, d_v]",
+                            "us": ms_lcont * 1e3,
+                            "frac": bpq * nq / (ms_lcont * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                            "us_cold_cache": ms_lcont_cold * 1e3,
+                            "frac_cold_cache": bpq * nq / (ms_lcont_cold * 1e-3) / 1e9
+                                               / HBM_PEAK_GBS}},
         "pack_kernel": {"kernel": "pack_tile_kernel, one layer's query codes",
                         "us": ms_p * 1e3, "rows": nq, "bytes_per_row": 2 * cfg.d_qk + 4,
                         "achieved_gbs": (2 * cfg.d_qk + 4) * nq / (ms_p * 1e-3) / 1e9,
