@@ -53,20 +53,32 @@ namespace {
 // (measured: 116 -> 112 us on B8 H16 T16384 Zipf codes; 307 -> 172 us, with the filter, on a
 // language-model layer of B4 H64 T16384 d 24). Otherwise every chunk of row r runs on XCD
 // r % 8, latest chunks first.
-__device__ __forceinline__ void item_rc(int nchunks, bool group, int v, int64_t& row, int& chunk) {
+// With `alt` every other group of 8 rows takes its chunks earliest first instead. A late
+// chunk's backward scan covers more earlier keys, so it costs more, and a persistent
+// workgroup b runs items b, b + G, ..., which with G = 8 groups' items (1024 items of 16
+// chunks) fall in consecutive groups at the same place: alternating hands it a late chunk and
+// then an early one instead of the same late chunk twice. The persistent kernel asks for it
+// when each workgroup has two items: on B8 H16 T16384 Zipf codes (d_v 64) the launch after a
+// cache eviction went from 111.2-111.7 to 105.9-107.5 us, back to back unchanged. With four
+// items (a language-model layer, B4 H64 T16384 d_v 24) alternating, and the pairs c, 15 - c,
+// 15 - c, c, both measured 4-6 us slower, so four-item grids keep the latest chunks first.
+__device__ __forceinline__ void item_rc(int nchunks, bool group, int v, int64_t& row, int& chunk,
+                                        bool alt = false) {
   const int xcd = v % kNumXcd;
   const int k = v / kNumXcd;
   if (group) {
     const int per = kNumXcd * nchunks;
-    chunk = nchunks - 1 - (k % per) / kNumXcd;
+    const int c = (k % per) / kNumXcd;
+    chunk = alt && ((k / per) & 1) ? c : nchunks - 1 - c;
     row = (static_cast<int64_t>(k / per) * kNumXcd + xcd) * kNumXcd + (k % per) % kNumXcd;
   } else {
     chunk = nchunks - 1 - (k % nchunks);
     row = static_cast<int64_t>(k / nchunks) * kNumXcd + xcd;
   }
 }
-__device__ __forceinline__ void item_of(const ResolveArgs& a, int v, int64_t& row, int& chunk) {
-  item_rc(a.nchunks, a.group != 0, v, row, chunk);
+__device__ __forceinline__ void item_of(const ResolveArgs& a, int v, int64_t& row, int& chunk,
+                                        bool alt = false) {
+  item_rc(a.nchunks, a.group != 0, v, row, chunk, alt);
 }
 
 // One workgroup (256 threads) per work item: resolve the chunk, then (VEC > 0) copy its value
@@ -105,7 +117,8 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
 // codes (d_v 64): 84.3 us with one workgroup per item, 77.5 us this way; on a language-model
 // layer (B4 H64 T16384, d_v 24): 104.1 and 91.0 us.
 template <typename CodeT, int VEC, bool kSumm>
-__global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_lag_kernel(ResolveArgs a, int32_t items) {
+__global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_lag_kernel(ResolveArgs a, int32_t items,
+                                                                                            int32_t alt) {
   static_assert(VEC > 0, "the persistent form exists for copies");
   __shared__ ResolveLds<CodeT> s;
   const int bid = blockIdx.x, G = gridDim.x;
@@ -125,7 +138,7 @@ __global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_
     asm volatile("" : "+v"(t));
     int64_t row = a.N;
     int chunk = 0;
-    if (i < n) item_of(a, bid + i * G, row, chunk);
+    if (i < n) item_of(a, bid + i * G, row, chunk, alt != 0);
     int32_t src[kPer] = {-1, -1, -1, -1};
     const bool resolved = row < a.N;
     if (resolved) {
@@ -389,7 +402,7 @@ int launch_items(ResolveArgs& a, int64_t items, hipStream_t st) {
       const int64_t k = (items + resident - 1) / resident;
       const int64_t g = ((items + k - 1) / k + kNumXcd - 1) / kNumXcd * kNumXcd;
       if (10 * g >= 9 * resident) {
-        lag<<<dim3(g), dim3(kThreads), 0, st>>>(a, static_cast<int32_t>(items));
+        lag<<<dim3(g), dim3(kThreads), 0, st>>>(a, static_cast<int32_t>(items), k == 2 ? 1 : 0);
         return launch_status("resolve_lag_kernel");
       }
     }
