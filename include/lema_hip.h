@@ -221,6 +221,17 @@ int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, const void*
                          int64_t K, int32_t d, int64_t T, void* qcodes, void* kcodes,
                          int32_t code_bytes, void* v, void* stream);
 
+/* A prefill's query and key projections straight to codes: qcodes and kcodes [M / T, N / d, T]
+ * (rows of x are M / T streams of T positions) of x [M, K] . wq^T and x . wk^T (wq, wk
+ * [N, K] bf16, row strides ldx, ldw), bit j of a head's code = (bf16(z_j) >= 0), z never
+ * stored. A persistent MFMA GEMM with the sign-pack in its epilogue. Replaces project +
+ * pack_codes (code/lema/model.py:168-175, code/lema/attention.py:82-97) on prefill shapes:
+ * M a multiple of 2048, N a multiple of 256, K of 64, d a multiple of 8 up to 64,
+ * code_bytes 4 for d <= 32 and 8 above. */
+int lema_qk_pack_bf16(const void* x, int64_t ldx, const void* wq, const void* wk, int64_t ldw,
+                      int64_t M, int64_t N, int64_t K, int32_t d, int64_t T, void* qcodes,
+                      void* kcodes, int32_t code_bytes, void* stream);
+
 /* out[M, N] = bf16(bf16(silu(g)) * u), g = bf16(x . wg^T), u = bf16(x . wu^T): the gate and
  * up projections and SwiGLU's product in one launch (code/lema/model.py:85-94), out row stride
  * N. */

@@ -56,6 +56,8 @@ PROTOTYPES = {
     "lema_skinny_gemm_bf16": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
     "lema_skinny_pack_bf16": ([_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _i64, _p, _i32, _p],
                               ctypes.c_int),
+    "lema_qk_pack_bf16": ([_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _i64, _p, _p, _i32,
+                           _p], ctypes.c_int),
     "lema_skinny_gemm_add_bf16": ([_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p],
                                   ctypes.c_int),
     "lema_skinny_qkv_bf16": ([_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i64,

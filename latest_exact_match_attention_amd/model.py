@@ -39,7 +39,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _lib
-from .attention import code_dtype_for, lema_hard, pack_codes
+from .attention import code_dtype_for, lema_from_codes, lema_hard, pack_codes
 
 __all__ = ["ModelConfig", "SwiGLU", "Attention", "Block", "Transformer", "lm_loss", "rms_norm",
            "embed", "argmax_into", "load_trained",
@@ -200,6 +200,36 @@ def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype, norm: nn.RMSNorm |
     return qc, kc, v.view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
 
 
+# Rows of a prefill projection taken by lema_qk_pack_bf16 (q and k straight to codes): its
+# 256 x 256 tiles cover the rows in 8 row groups, one per XCD.
+QK_PACK_ROWS = 2048
+
+
+def project_qk_prefill(x: torch.Tensor, at, code_dtype: torch.dtype):
+    """[B, T, dim] -> (qc, kc [B, H, T] codes) of a prefill-sized input (B * T a multiple of
+    2048 rows, bf16, no autograd): the query and key projections and the sign-pack in one
+    persistent MFMA launch whose epilogue writes the codes, so the pre-activations zq and zk
+    never reach memory. The same codes as project + pack_codes (bit j = bf16(z_j) >= 0); None
+    where the launch does not apply (the caller then projects and packs)."""
+    c = at.cfg
+    wq, wk = at.q_proj.weight, at.k_proj.weight
+    if torch.is_grad_enabled() and (x.requires_grad or wq.requires_grad or wk.requires_grad):
+        return None
+    if not (_fused(x, wq, wk) and x.dim() == 3 and wq.shape == wk.shape):
+        return None
+    B, T, K = x.shape
+    N, d = wq.shape[0], c.d_qk
+    if ((B * T) % QK_PACK_ROWS or N % 256 or K % 64 or d % 8 or d > 64 or N % d
+            or x.data_ptr() % 16 or wq.data_ptr() % 16 or wk.data_ptr() % 16):
+        return None
+    qc = torch.empty((B, N // d, T), dtype=code_dtype, device=x.device)
+    kc = torch.empty_like(qc)
+    _lib.check(_lib.lib().lema_qk_pack_bf16(
+        x.data_ptr(), K, wq.data_ptr(), wk.data_ptr(), K, B * T, N, K, d, T, qc.data_ptr(),
+        kc.data_ptr(), qc.element_size(), _lib.stream_of(x)))
+    return qc, kc
+
+
 ATTN_KINDS = ("lema",)
 POS_KINDS = ("nope",)
 
@@ -355,6 +385,12 @@ class Attention(nn.Module):
         if not self.hard:
             raise NotImplementedError("only the exact (hard) op is implemented: call "
                                       "model.set_hard(True)")
+        codes = project_qk_prefill(x, self, code_dtype_for(self.cfg.d_qk))
+        if codes is not None:  # q and k straight to codes; v by its own product
+            B, T, _ = x.shape
+            c = self.cfg
+            v = linear(x, self.v_proj).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
+            return self.merge(lema_from_codes(codes[0], codes[1], v))
         zq, zk, v = self.project(x)
         return self.merge(lema_hard(zq, zk, v))
 
@@ -377,7 +413,8 @@ class Block(nn.Module):
     def gpu_pre(self, x):
         """Normalise, project, pack both codes (code/lema/model.py:224-227). On decode shapes
         the norm and the three projections are one launch, q and k going straight to codes
-        (skinny MFMA kernel: pre-norm prologue, pack epilogues)."""
+        (skinny MFMA kernel: pre-norm prologue, pack epilogues); on prefill chunks of 2048 or
+        more rows q and k go straight to codes in one persistent MFMA launch."""
         at, c = self.attn, self.attn.cfg
         ct = code_dtype_for(c.d_qk)
         fused = project_qkv(x, at, ct, norm=self.norm1)
@@ -387,6 +424,11 @@ class Block(nn.Module):
         fused = project_qkv(h, at, ct)
         if fused is not None:
             return fused
+        codes = project_qk_prefill(h, at, ct)
+        if codes is not None:  # prefill chunks of 2048+ rows
+            B, T, _ = h.shape
+            v = linear(h, at.v_proj).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)
+            return codes[0], codes[1], v
         qc = project_codes(h, at.q_proj, c.d_qk, ct)
         kc = project_codes(h, at.k_proj, c.d_qk, ct) if qc is not None else None
         if kc is not None:
