@@ -576,7 +576,8 @@ def bench_lm(a):
     import torch
     from latest_exact_match_attention_amd import build, pack_codes
     from latest_exact_match_attention_amd.attention import launch_hard
-    from latest_exact_match_attention_amd.model import ModelConfig, Transformer, lm_loss
+    from latest_exact_match_attention_amd.model import (ModelConfig, Transformer, lm_loss,
+                                                        project_qk_prefill)
 
     if not build.LIB.exists():
         build.build()
@@ -649,6 +650,34 @@ def bench_lm(a):
         e1.record(stream)
         torch.cuda.synchronize()
         ms_p = e0.elapsed_time(e1) / n_l
+        # one layer's q and k codes: both projections straight to codes in one launch (the
+        # model's FUSED_QK_PACK, off), against the library path the forward takes (two
+        # hipBLASLt GEMMs writing zq and zk, two packs)
+        hn = blk.norm1(model.tok_emb(x))
+        at = blk.attn
+
+        def unfused_qk():
+            a_, b_, _ = hn.shape
+            zq_ = at.q_proj(hn).view(a_, b_, cfg.num_heads, cfg.d_qk).transpose(1, 2)
+            zk_ = at.k_proj(hn).view(a_, b_, cfg.num_heads, cfg.d_qk).transpose(1, 2)
+            return pack_codes(zq_, torch.int32), pack_codes(zk_, torch.int32)
+
+        fused_qk = lambda: project_qk_prefill(hn, at, torch.int32)
+        fq, fk = fused_qk()
+        uq, uk = unfused_qk()
+        qk_same = bool(torch.equal(fq, uq) and torch.equal(fk, uk))
+        del uq, uk
+        ms_qk = {}
+        for name, fn in (("fused", fused_qk), ("library", unfused_qk)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(n_l):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms_qk[name] = e0.elapsed_time(e1) / n_l
     ntok = B * T
     flops = lm_flops_per_token(cfg) * ntok
     tflops = flops / (ms * 1e-3) / 1e12
@@ -689,6 +718,15 @@ def bench_lm(a):
                             "us_cold_cache": ms_lcont_cold * 1e3,
                             "frac_cold_cache": bpq * nq / (ms_lcont_cold * 1e-3) / 1e9
                                                / HBM_PEAK_GBS}},
+        "qk_pack_kernel": {
+            "kernel": "qk_pack_kernel (q and k projections straight to codes), one layer",
+            "us": ms_qk["fused"] * 1e3,
+            "tflops": 2 * B * T * 2 * cfg.dim * cfg.dim / (ms_qk["fused"] * 1e-3) / 1e12,
+            "frac": 2 * B * T * 2 * cfg.dim * cfg.dim / (ms_qk["fused"] * 1e-3) / 1e12
+                    / MFMA_BF16_PEAK_TFLOPS,
+            "library_path_us": ms_qk["library"] * 1e3,
+            "library_path": "two hipBLASLt GEMMs (zq, zk to HBM) and two pack_tile_kernel",
+            "codes_identical": qk_same},
         "pack_kernel": {"kernel": "pack_tile_kernel, one layer's query codes",
                         "us": ms_p * 1e3, "rows": nq, "bytes_per_row": 2 * cfg.d_qk + 4,
                         "achieved_gbs": (2 * cfg.d_qk + 4) * nq / (ms_p * 1e-3) / 1e9,

@@ -12,13 +12,17 @@
 // memory phase (all fragments of a 64-deep stage read from LDS into registers; group 0 also
 // issues the next stage's global -> LDS loads, buffer_load ... lds, into the other of two
 // 64 KB stages) and a compute phase (32 MFMAs), so each SIMD always has one wave in MFMA. The
-// epilogue turns each row's 32 column signs of an MFMA tile into one word (the lane pair
-// holding the row combines its halves) and stores the code bytes: d is a multiple of 8, so a
-// byte of a code never straddles a tile, and the writer of a code's last byte clears the bytes
-// above d.
+// epilogue turns each row's 32 column signs of an MFMA tile into one word (two instructions
+// per sign; the lane pair holding the row combines its halves) and stores the code bytes: d is
+// a multiple of 8, so a byte of a code never straddles a tile, and the writer of a code's last
+// byte clears the bytes above d. The epilogue runs while the other group computes, so its
+// instruction count sets what it costs: ~500 VALU instructions per tile and wave.
 //
 // Measured on the language model's shape (x [65536, 1536], Wq and Wk [1536, 1536], 64 heads
-// of 24 bits): see the entry point.
+// of 24 bits, the model's layer-0 input), alternating with the unfused path on one device:
+// 494.5 us (1.25 PFLOP/s) against 526 us for two hipBLASLt GEMMs and two packs, codes
+// identical; 523 us with an epilogue of ~1230 instructions (a bf16 conversion and two compares
+// per pair of signs, 64-bit divisions for the addresses).
 #include "lema_internal.h"
 
 namespace lema {
@@ -52,14 +56,21 @@ struct QkArgs {
   int32_t M, N, K, ldx, ldw;
   int32_t d, T, H, code_bytes;
   int32_t tiles_m, tiles_n, gm;
+  int32_t db, hstride;  // code bytes in use (d / 8); T * code_bytes
+  float inv_db;
+  int64_t bstride;      // one stream's codes: H * T * code_bytes
 };
 
-// bit = (bf16(z) >= 0) with the hardware's round-to-nearest-even conversion: -0 counts as
-// non-negative and NaN does not, as in pack_codes
-__device__ __forceinline__ uint32_t sign_bits2(float a, float b) {
-  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
-  const float fa = __uint_as_float(h << 16), fb = __uint_as_float(h & 0xFFFF0000u);
-  return (fa >= 0.0f ? 1u : 0u) | (fb >= 0.0f ? 2u : 0u);
+// w * 2 + (bf16(z) >= 0): for every fp32 z, NaN included, bf16(z) >= 0 under round to nearest
+// even is z >= -2^-134 (a tie at 2^-134 rounds to -0, and fp32 denormals are kept), so one
+// compare into VCC and an add that takes VCC as its carry in push the bit
+__device__ __forceinline__ uint32_t push_sign(uint32_t w, float z, uint32_t thr) {
+  uint32_t r;
+  asm("v_cmp_le_f32_e32 vcc, %2, %1\n\tv_addc_co_u32_e32 %0, vcc, %3, %3, vcc"
+      : "=v"(r)
+      : "v"(z), "s"(thr), "v"(w)
+      : "vcc");
+  return r;
 }
 
 __global__ __launch_bounds__(kQkThreads, 1) void qk_pack_kernel(QkArgs g) {
@@ -157,39 +168,60 @@ __global__ __launch_bounds__(kQkThreads, 1) void qk_pack_kernel(QkArgs g) {
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk][j], fa[kk][i], acc[i][j], 0, 0, 0);
   };
+  const int h = l >> 5;
+  const uint32_t thr = __builtin_amdgcn_readfirstlane(0x80008000u);
   auto epilogue = [&](int it) __attribute__((always_inline)) {
     int m0, n0;
     tile_of(it, m0, n0);
     const bool isq = n0 < g.N;
     uint8_t* codes = static_cast<uint8_t*>(isq ? g.qc : g.kc);
-    const int c0 = (isq ? n0 : n0 - g.N) + wc;  // the wave's first column within q or k
-    const int h = l >> 5;
+    // the byte of 8 columns gi = (this lane's first) + 4 j + y is byte gi % db of head gi / db
+    // ((gi + 0.5) / db in fp32 is exact for gi < 2^13)
+    const int gb = (((isq ? n0 : n0 - g.N) + wc) >> 3) + 2 * h;
+    int coff[4][2];
+    bool last[4][2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        const int gi = gb + 4 * j + y;
+        const int head = static_cast<int>((static_cast<float>(gi) + 0.5f) * g.inv_db);
+        const int kb = gi - head * g.db;
+        coff[j][y] = head * g.hstride + kb;
+        last[j][y] = kb == g.db - 1;
+      }
+    const __amdgpu_buffer_rsrc_t rc =
+        __builtin_amdgcn_make_buffer_rsrc(codes, 0, 0x7FFFFFFF, 0x00020000);
+    uint32_t roff[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int64_t row = m0 + wr + i * 32 + fr;
-      const int64_t b = row / g.T, tt = row - b * g.T;
+      const uint32_t row = static_cast<uint32_t>(m0 + wr + i * 32 + fr);
+      const uint32_t b = row / static_cast<uint32_t>(g.T);
+      roff[i] = b * static_cast<uint32_t>(g.bstride) + (row - b * g.T) * g.code_bytes;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t m = 0;
+        // column 8 q + 4 h + e of the row (acc[i][j][4 q + e]) lands in bit 8 q + 4 h + e
+        uint32_t w = 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 3; q >= 0; --q) {
 #pragma unroll
-          for (int e = 0; e < 4; e += 2)
-            m |= sign_bits2(acc[i][j][4 * q + e], acc[i][j][4 * q + e + 1]) << (8 * q + 4 * h + e);
-        m |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 32));  // the row's 32 signs
-        // lanes of half h store bytes 2 h and 2 h + 1 of the word (8 columns each)
+          for (int e = 3; e >= 0; --e) w = push_sign(w, acc[i][j][4 * q + e], thr);
+          if (q) w <<= 4;
+        }
+        w <<= 4 * h;
+        const uint32_t m = w | static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), 32));
 #pragma unroll
         for (int y = 0; y < 2; ++y) {
-          const int q = 2 * h + y;
-          const int c = c0 + j * 32 + 8 * q;
-          const int head = c / g.d, kb = (c - head * g.d) >> 3;
-          uint8_t* p = codes + ((b * g.H + head) * g.T + tt) * g.code_bytes;
-          p[kb] = static_cast<uint8_t>(m >> (8 * q));
-          if (kb == (g.d >> 3) - 1)
-            for (int z = kb + 1; z < g.code_bytes; ++z) p[z] = 0;
+          const uint32_t o = roff[i] + coff[j][y];
+          __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(m >> (8 * (2 * h + y))), rc, o, 0, 0);
+          if (last[j][y])
+            for (int z = 1; z < g.code_bytes - g.db + 1; ++z)
+              __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(0), rc, o + z, 0, 0);
         }
       }
-    }
   };
 
   // Group 0 runs M(0) C(0) M(1) C(1) ..., group 1 the same one phase later. Stage s + 1 goes
@@ -239,9 +271,9 @@ extern "C" int lema_qk_pack_bf16(const void* x, int64_t ldx, const void* wq, con
   clear_error();
   LEMA_REQUIRE(M > 0 && M % (8 * kQkBM) == 0 && M < (int64_t(1) << 31),
                "rows %lld must be a positive multiple of %d", (long long)M, 8 * kQkBM);
-  LEMA_REQUIRE(N > 0 && N % kQkBN == 0 && N < (int64_t(1) << 30),
-               "columns per projection %lld must be a positive multiple of %d", (long long)N,
-               kQkBN);
+  LEMA_REQUIRE(N > 0 && N % kQkBN == 0 && N <= 65536,
+               "columns per projection %lld must be a positive multiple of %d, at most 65536",
+               (long long)N, kQkBN);
   LEMA_REQUIRE(K >= kQkBK && K % kQkBK == 0 && K < (int64_t(1) << 20),
                "K=%lld must be a multiple of %d", (long long)K, kQkBK);
   LEMA_REQUIRE(d > 0 && d <= 64 && d % 8 == 0 && N % d == 0,
@@ -250,6 +282,8 @@ extern "C" int lema_qk_pack_bf16(const void* x, int64_t ldx, const void* wq, con
                d <= 32 ? 4 : 8);
   LEMA_REQUIRE(T > 0 && M % T == 0, "rows %lld must be whole streams of %lld", (long long)M,
                (long long)T);
+  LEMA_REQUIRE(M / d * N * code_bytes < (int64_t(1) << 31), "codes of %lld bytes: at most 2 GiB",
+               (long long)(M / d * N * code_bytes));
   LEMA_REQUIRE(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 && ldx < (1 << 20) &&
                    ldw < (1 << 20),
                "row strides must be >= K and multiples of 8");
@@ -275,6 +309,10 @@ extern "C" int lema_qk_pack_bf16(const void* x, int64_t ldx, const void* wq, con
   g.tiles_n = static_cast<int32_t>(2 * N / kQkBN);
   const int per_x = g.tiles_m / 8;
   g.gm = per_x % 4 == 0 ? 4 : per_x % 2 == 0 ? 2 : 1;
+  g.db = d / 8;
+  g.inv_db = 1.0f / static_cast<float>(g.db);
+  g.hstride = static_cast<int32_t>(T * code_bytes);
+  g.bstride = static_cast<int64_t>(N / d) * T * code_bytes;
   const int cus = num_cus();
   LEMA_REQUIRE(cus >= 8 && cus % 8 == 0, "%d compute units: the tile order needs whole XCDs", cus);
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -203,6 +203,13 @@ def project_qkv(x: torch.Tensor, at, code_dtype: torch.dtype, norm: nn.RMSNorm |
 # Rows of a prefill projection taken by lema_qk_pack_bf16 (q and k straight to codes): its
 # 256 x 256 tiles cover the rows in 8 row groups, one per XCD.
 QK_PACK_ROWS = 2048
+# Whether the model's prefill takes its q and k codes from lema_qk_pack_bf16 (the codes are
+# identical either way). Off: on the 4 x 16384-token, dim-1536 prefill the launch takes
+# 494.5-541 us against 526-560 us for the two hipBLASLt GEMMs and two packs when timed alone,
+# but 572 us against 525 us inside the forward, where both run at the clock a sustained matrix
+# load holds (it spends ~30% more cycles per FLOP than the library's GEMMs); the forward's step
+# time is the same with it on or off (114.5-114.8 ms).
+FUSED_QK_PACK = False
 
 
 def project_qk_prefill(x: torch.Tensor, at, code_dtype: torch.dtype):
@@ -219,7 +226,9 @@ def project_qk_prefill(x: torch.Tensor, at, code_dtype: torch.dtype):
         return None
     B, T, K = x.shape
     N, d = wq.shape[0], c.d_qk
-    if ((B * T) % QK_PACK_ROWS or N % 256 or K % 64 or d % 8 or d > 64 or N % d
+    cb = torch.empty((), dtype=code_dtype).element_size()
+    if ((B * T) % QK_PACK_ROWS or N % 256 or N > 65536 or K % 64 or d % 8 or d > 64 or N % d
+            or cb != (4 if d <= 32 else 8) or B * T * (N // d) * cb >= 1 << 31
             or x.data_ptr() % 16 or wq.data_ptr() % 16 or wk.data_ptr() % 16):
         return None
     qc = torch.empty((B, N // d, T), dtype=code_dtype, device=x.device)
@@ -385,7 +394,8 @@ class Attention(nn.Module):
         if not self.hard:
             raise NotImplementedError("only the exact (hard) op is implemented: call "
                                       "model.set_hard(True)")
-        codes = project_qk_prefill(x, self, code_dtype_for(self.cfg.d_qk))
+        codes = (project_qk_prefill(x, self, code_dtype_for(self.cfg.d_qk))
+                 if FUSED_QK_PACK else None)
         if codes is not None:  # q and k straight to codes; v by its own product
             B, T, _ = x.shape
             c = self.cfg
@@ -413,8 +423,9 @@ class Block(nn.Module):
     def gpu_pre(self, x):
         """Normalise, project, pack both codes (code/lema/model.py:224-227). On decode shapes
         the norm and the three projections are one launch, q and k going straight to codes
-        (skinny MFMA kernel: pre-norm prologue, pack epilogues); on prefill chunks of 2048 or
-        more rows q and k go straight to codes in one persistent MFMA launch."""
+        (skinny MFMA kernel: pre-norm prologue, pack epilogues); with FUSED_QK_PACK set, on
+        prefill chunks of 2048 or more rows q and k go straight to codes in one persistent
+        MFMA launch."""
         at, c = self.attn, self.attn.cfg
         ct = code_dtype_for(c.d_qk)
         fused = project_qkv(x, at, ct, norm=self.norm1)
@@ -424,7 +435,7 @@ class Block(nn.Module):
         fused = project_qkv(h, at, ct)
         if fused is not None:
             return fused
-        codes = project_qk_prefill(h, at, ct)
+        codes = project_qk_prefill(h, at, ct) if FUSED_QK_PACK else None
         if codes is not None:  # prefill chunks of 2048+ rows
             B, T, _ = h.shape
             v = linear(h, at.v_proj).view(B, T, c.num_kv_heads, c.d_v).transpose(1, 2)

@@ -1,7 +1,8 @@
 """The prefill's query and key projections straight to codes (lema_qk_pack_bf16: a persistent
 MFMA GEMM whose epilogue packs the signs) against torch's bf16 product packed by the oracle's
-pack_codes restatement (code/lema/attention.py:82-97), through the C ABI, and inside the model:
-Attention.forward and a cached prefill in chunks of 2048 rows give the unfused path's output.
+pack_codes restatement (code/lema/attention.py:82-97), through the C ABI, and inside the model
+with FUSED_QK_PACK set (it is off by default): Attention.forward and a cached prefill in chunks
+of 2048 rows give the unfused path's output.
 
 The two products sum in the same order, so the codes are expected to be identical; the stated
 binarization tolerance still bounds what may differ: a bit only where its fp32 pre-activation
@@ -74,6 +75,7 @@ def test_shapes_outside_the_tiles_are_refused(dev):
                              8, 2048, c.data_ptr(), c.data_ptr(), 4, s)
     assert ok == _lib.OK
     for args in ((1024, 256, 128, 8, 1024, 4), (2048, 128, 128, 8, 2048, 4),
+                 (2048, 65536 + 256, 128, 8, 2048, 4),
                  (2048, 256, 96, 8, 2048, 4), (2048, 256, 128, 12, 2048, 4),
                  (2048, 256, 128, 40, 2048, 4), (2048, 256, 128, 8, 1000, 4)):
         M, N, K, d, T, cb = args
@@ -97,9 +99,11 @@ def _model(dev, T):
     return m, cfg
 
 
-def test_attention_forward_equals_the_unfused_path(dev):
-    """Attention.forward on a 2 x 2048-token prefill takes the fused codes; its output equals
-    project + lema_hard + merge bit for bit."""
+def test_attention_forward_equals_the_unfused_path(dev, monkeypatch):
+    """Attention.forward on a 2 x 2048-token prefill with FUSED_QK_PACK set takes the fused
+    codes; its output equals project + lema_hard + merge bit for bit."""
+    import latest_exact_match_attention_amd.model as model_mod
+    monkeypatch.setattr(model_mod, "FUSED_QK_PACK", True)
     m, cfg = _model(dev, 2048)
     at = m.blocks[0].attn
     with torch.no_grad():
@@ -111,11 +115,12 @@ def test_attention_forward_equals_the_unfused_path(dev):
 
 
 def test_cached_prefill_in_2048_row_chunks(dev, monkeypatch):
-    """A cached forward fed 2 x 4096 tokens in chunks of 1024 positions (2048 rows each: the
-    fused codes in Block.gpu_pre) gives bit for bit the logits and the table of the same
-    cached forward with the codes from project + pack_codes; and the dense forward's logits
-    within bf16 rounding."""
+    """A cached forward fed 2 x 4096 tokens in chunks of 1024 positions (2048 rows each: with
+    FUSED_QK_PACK set, the fused codes in Block.gpu_pre) gives bit for bit the logits and the
+    table of the same cached forward with the codes from project + pack_codes; and the dense
+    forward's logits within bf16 rounding."""
     import latest_exact_match_attention_amd.model as model_mod
+    monkeypatch.setattr(model_mod, "FUSED_QK_PACK", True)
     m, cfg = _model(dev, 4096)
     x = torch.randint(0, 512, (2, 4096), device=dev)
 
@@ -127,7 +132,7 @@ def test_cached_prefill_in_2048_row_chunks(dev, monkeypatch):
     with torch.no_grad():
         dense = m(x)
         fused, c1 = cached()
-        monkeypatch.setattr(model_mod, "QK_PACK_ROWS", 1 << 40)     # no fused codes
+        monkeypatch.setattr(model_mod, "FUSED_QK_PACK", False)      # no fused codes
         plain, c2 = cached()
     assert torch.equal(fused.view(torch.int16), plain.view(torch.int16))
     assert torch.equal(c1.counts(), c2.counts()) and c1.entries() == c2.entries() > 0
