@@ -47,7 +47,8 @@ def check_against_product(got, x, w, d, T):
 
 @pytest.mark.parametrize("M,T,K,N,d", [(2048, 2048, 64, 256, 8), (4096, 1024, 128, 512, 32),
                                        (2048, 256, 192, 768, 24), (2048, 512, 128, 256, 64),
-                                       (4096, 4096, 64, 1280, 40), (8192, 2048, 1536, 1536, 24)])
+                                       (4096, 4096, 64, 1280, 40), (8192, 2048, 1536, 1536, 24),
+                                       (2048, 128, 64, 512, 16)])   # streams shorter than a tile
 def test_codes_equal_the_packed_product(dev, M, T, K, N, d):
     g = torch.Generator(device=dev).manual_seed(M + N + d)
     x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
