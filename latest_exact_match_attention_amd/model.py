@@ -226,7 +226,7 @@ def project_qk_prefill(x: torch.Tensor, at, code_dtype: torch.dtype):
         return None
     B, T, K = x.shape
     N, d = wq.shape[0], c.d_qk
-    cb = torch.empty((), dtype=code_dtype).element_size()
+    cb = torch.iinfo(code_dtype).bits // 8
     if ((B * T) % QK_PACK_ROWS or N % 256 or N > 65536 or K % 64 or d % 8 or d > 64 or N % d
             or cb != (4 if d <= 32 else 8) or B * T * (N // d) * cb >= 1 << 31
             or x.data_ptr() % 16 or wq.data_ptr() % 16 or wk.data_ptr() % 16):
