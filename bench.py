@@ -667,17 +667,21 @@ def bench_lm(a):
         uq, uk = unfused_qk()
         qk_same = bool(torch.equal(fq, uq) and torch.equal(fk, uk))
         del uq, uk
-        ms_qk = {}
-        for name, fn in (("fused", fused_qk), ("library", unfused_qk)):
-            for _ in range(3):
-                fn()
-            torch.cuda.synchronize()
-            e0.record(stream)
-            for _ in range(n_l):
-                fn()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            ms_qk[name] = e0.elapsed_time(e1) / n_l
+        # three rounds, the two paths alternating, medians (a path's first round after the
+        # other reads slow while the clocks settle)
+        rounds = {"fused": [], "library": []}
+        for _ in range(3):
+            for name, fn in (("fused", fused_qk), ("library", unfused_qk)):
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+                e0.record(stream)
+                for _ in range(n_l):
+                    fn()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                rounds[name].append(e0.elapsed_time(e1) / n_l)
+        ms_qk = {k: sorted(v)[1] for k, v in rounds.items()}
     ntok = B * T
     flops = lm_flops_per_token(cfg) * ntok
     tflops = flops / (ms * 1e-3) / 1e12
@@ -725,6 +729,7 @@ def bench_lm(a):
             "frac": 2 * B * T * 2 * cfg.dim * cfg.dim / (ms_qk["fused"] * 1e-3) / 1e12
                     / MFMA_BF16_PEAK_TFLOPS,
             "library_path_us": ms_qk["library"] * 1e3,
+            "rounds_us": {k: [round(x * 1e3, 1) for x in v] for k, v in rounds.items()},
             "library_path": "two hipBLASLt GEMMs (zq, zk to HBM) and two pack_tile_kernel",
             "codes_identical": qk_same},
         "pack_kernel": {"kernel": "pack_tile_kernel, one layer's query codes",
