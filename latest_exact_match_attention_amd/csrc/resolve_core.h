@@ -100,11 +100,13 @@ struct ResolveLds {
   alignas(16) uint64_t mbits[kMapSlots];  // lanes of that word whose key carries that code
   alignas(16) CodeT code[kSlots];         // query code of a slot, sentinel() = free
   alignas(16) uint32_t mkey[kMapSlots];   // code slot << 4 | word, kMapEmpty = free
-  int32_t pos[kSlots + 1];    // latest key position before the chunk, -1 = none; the entry
-                              // [kSlots] here and in summ belongs to the sentinel code itself
-  alignas(4) uint16_t summ[kSlots + 2];  // bit w: word w of the chunk holds a key with this
-                                         // code; updated as 32-bit pairs
-  uint32_t qbits[kFilterWords];  // bit filter_hash(c) set for every query code c of the chunk
+  alignas(16) int32_t pos[kSlots + 1];  // latest key position before the chunk, -1 = none;
+                                        // the entry [kSlots] here and in summ belongs to the
+                                        // sentinel code itself
+  alignas(16) uint16_t summ[kSlots + 2];  // bit w: word w of the chunk holds a key with this
+                                          // code; updated as 32-bit pairs
+  alignas(16) uint32_t qbits[kFilterWords];  // bit filter_hash(c) set for every query code c of
+                                             // the chunk
   int32_t sent_used;
   int32_t nq;     // distinct query codes of the chunk (the all-ones code aside)
   int32_t nneed;  // query codes that need their latest key before the chunk (summary path)
@@ -603,17 +605,26 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       if (c0 - (d + 1) * kBatch >= 0) load_batch(nxt[d], c0 - (d + 1) * kBatch);
   }
 
-  for (int x = t; x < kSlots; x += kThreads) s.code[x] = SENT;
-  for (int x = t; x <= kSlots; x += kThreads) {
-    s.pos[x] = -1;
-    s.summ[x] = 0;
+  {  // the tables cleared with 16-byte stores (the sentinel, -1 and kMapEmpty are all ones)
+    static_assert(kSlots % 8 == 0 && kMapSlots % 4 == 0 && kFilterWords % 4 == 0 &&
+                      kMapEmpty == 0xFFFFFFFFu,
+                  "16-byte clears");
+    const u32x4 ones = {~0u, ~0u, ~0u, ~0u}, zero = {0u, 0u, 0u, 0u};
+    auto fill = [&](void* base, int n16, u32x4 v) {
+      u32x4* q4 = reinterpret_cast<u32x4*>(base);
+      for (int x = t; x < n16; x += kThreads) q4[x] = v;
+    };
+    fill(s.code, kSlots * static_cast<int>(sizeof(CodeT)) / 16, ones);
+    fill(s.pos, kSlots / 4, ones);
+    fill(s.summ, kSlots / 8, zero);
+    fill(s.mkey, kMapSlots / 4, ones);
+    fill(s.mbits, kMapSlots / 2, zero);
+    fill(s.qbits, kFilterWords / 4, zero);
   }
-  for (int x = t; x < kMapSlots; x += kThreads) {
-    s.mkey[x] = kMapEmpty;
-    s.mbits[x] = 0;
-  }
-  for (int x = t; x < kFilterWords; x += kThreads) s.qbits[x] = 0;
   if (t == 0) {
+    s.pos[kSlots] = -1;
+    s.summ[kSlots] = 0;
+    s.summ[kSlots + 1] = 0;
     s.sent_used = 0;
     s.nq = 0;
     s.nneed = 0;
