@@ -605,15 +605,16 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       if (c0 - (d + 1) * kBatch >= 0) load_batch(nxt[d], c0 - (d + 1) * kBatch);
   }
 
-  {  // the tables cleared with 16-byte stores (the sentinel, -1 and kMapEmpty are all ones)
-    static_assert(kSlots % 8 == 0 && kMapSlots % 4 == 0 && kFilterWords % 4 == 0 &&
-                      kMapEmpty == 0xFFFFFFFFu,
-                  "16-byte clears");
-    const u32x4 ones = {~0u, ~0u, ~0u, ~0u}, zero = {0u, 0u, 0u, 0u};
-    auto fill = [&](void* base, int n16, u32x4 v) {
-      u32x4* q4 = reinterpret_cast<u32x4*>(base);
-      for (int x = t; x < n16; x += kThreads) q4[x] = v;
-    };
+  // the tables are cleared with 16-byte stores (the sentinel, -1 and kMapEmpty are all ones)
+  static_assert(kSlots % 8 == 0 && kMapSlots % 4 == 0 && kFilterWords % 4 == 0 &&
+                    kMapEmpty == 0xFFFFFFFFu,
+                "16-byte clears");
+  const u32x4 ones = {~0u, ~0u, ~0u, ~0u}, zero = {0u, 0u, 0u, 0u};
+  auto fill = [&](void* base, int n16, u32x4 v) {
+    u32x4* q4 = reinterpret_cast<u32x4*>(base);
+    for (int x = t; x < n16; x += kThreads) q4[x] = v;
+  };
+  {
     fill(s.code, kSlots * static_cast<int>(sizeof(CodeT)) / 16, ones);
     fill(s.pos, kSlots / 4, ones);
     fill(s.summ, kSlots / 8, zero);
@@ -821,11 +822,10 @@ __device__ __forceinline__ void resolve_chunk(ResolveLds<CodeT>& s, const Resolv
       fast = s.khit == 0;
       if (!fast) {
         // the map and the word summaries start over for the keys inside the chunk
-        for (int x = t; x < kMapSlots; x += kThreads) {
-          s.mkey[x] = kMapEmpty;
-          s.mbits[x] = 0;
-        }
-        for (int x = t; x <= kSlots; x += kThreads) s.summ[x] = 0;
+        fill(s.mkey, kMapSlots / 4, ones);
+        fill(s.mbits, kMapSlots / 2, zero);
+        fill(s.summ, kSlots / 8, zero);
+        if (t == 0) s.summ[kSlots] = 0;
         bar();
         keys_in_chunk(sl);
       }
