@@ -116,13 +116,22 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
 // them a chunk behind, resolving and copying run side by side. Measured on B8 H16 T16384 Zipf
 // codes (d_v 64): 84.3 us with one workgroup per item, 77.5 us this way; on a language-model
 // layer (B4 H64 T16384, d_v 24): 104.1 and 91.0 us.
+// Which half lags (`mode` bit 1): workgroups are dealt to the 8 XCDs in turn, and where each
+// XCD spreads its share over its 32 CUs in order, a block of 128 takes one slot on half of
+// every XCD's CUs, so lagging every other block (bid >> 7 odd) makes whole CUs lag, and every
+// other block of 256 (bid >> 8 odd) lags two of each CU's four workgroups instead. Long value rows favour the second (B8 H16 T16384 Zipf codes,
+// d_v 64: 79.8-80.8 against 81.2-81.3 us back to back, 100.9-101.4 against 104.9-105.0 us
+// after a cache eviction; with y interleaved 117.5 against 120.3 us and 107.5 against 112),
+// short ones the first (language-model layer, d_v 24, y interleaved: 91.8-92.1 against
+// 94.1-94.3 us at B4; after an eviction 63.5 against 66.3 us at B2).
+// `mode` bit 0 asks item_of for alternating chunk order.
 template <typename CodeT, int VEC, bool kSumm>
 __global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_lag_kernel(ResolveArgs a, int32_t items,
-                                                                                            int32_t alt) {
+                                                                                            int32_t mode) {
   static_assert(VEC > 0, "the persistent form exists for copies");
   __shared__ ResolveLds<CodeT> s;
   const int bid = blockIdx.x, G = gridDim.x;
-  const bool lagged = (bid >> 7) & 1;
+  const bool lagged = (mode & 2) ? (bid >> 8) & 1 : (bid >> 7) & 1;
   auto bar = [] { __syncthreads(); };
   int32_t* srcs = reinterpret_cast<int32_t*>(s.mbits);  // the masks are dead while copying
   const int n = bid < items ? (items - bid + G - 1) / G : 0;
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_
     asm volatile("" : "+v"(t));
     int64_t row = a.N;
     int chunk = 0;
-    if (i < n) item_of(a, bid + i * G, row, chunk, alt != 0);
+    if (i < n) item_of(a, bid + i * G, row, chunk, (mode & 1) != 0);
     int32_t src[kPer] = {-1, -1, -1, -1};
     const bool resolved = row < a.N;
     if (resolved) {
@@ -392,6 +401,10 @@ int64_t resident_groups(K kernel, std::atomic<int> (&per_dev)[kMaxDev]) {
 // the dispatcher fills the slots as they free up (measured striped: 1152 items on 1024 slots
 // 45.8 against 38.6 us one per item; 2048 items of 8-byte codes on 768 slots, 89.0 against
 // 75.1 us).
+// Value rows of at least this many bytes lag two workgroups of every CU, shorter ones whole
+// CUs (resolve_lag_kernel's `mode` bit 1; measured at 128- and 48-byte rows).
+constexpr uint32_t kMixedLagRowBytes = 128;
+
 template <typename CodeT, int VEC, bool kSumm>
 int launch_items(ResolveArgs& a, int64_t items, hipStream_t st) {
   if constexpr (VEC > 0) {
@@ -402,7 +415,8 @@ int launch_items(ResolveArgs& a, int64_t items, hipStream_t st) {
       const int64_t k = (items + resident - 1) / resident;
       const int64_t g = ((items + k - 1) / k + kNumXcd - 1) / kNumXcd * kNumXcd;
       if (10 * g >= 9 * resident) {
-        lag<<<dim3(g), dim3(kThreads), 0, st>>>(a, static_cast<int32_t>(items), k == 2 ? 1 : 0);
+        const int32_t mode = (k == 2 ? 1 : 0) | (a.g.pieces * VEC >= kMixedLagRowBytes ? 2 : 0);
+        lag<<<dim3(g), dim3(kThreads), 0, st>>>(a, static_cast<int32_t>(items), mode);
         return launch_status("resolve_lag_kernel");
       }
     }
