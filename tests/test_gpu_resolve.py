@@ -260,6 +260,7 @@ def test_value_row_shapes(dev, dv, dtype):
 @pytest.mark.parametrize("N,T,code_dtype,dv", [
     (72, 27000, torch.int32, 24),    # 1944 items on 976 workgroups: some take 2, some 1
     (64, 29500, torch.int32, 64),    # grouped order, a partial last chunk
+    (100, 29000, torch.int32, 64),   # 2900 items, 3 per workgroup, 128-byte value rows
     (128, 12000, torch.int64, 32),   # 8-byte codes: 3 workgroups per CU
     (16, 131072, torch.int32, 8),    # 128 chunks per row: the chunk summaries
 ])
