@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
 
 // Persistent form of resolve_kernel with copies. As many workgroups as the GPU holds at once
 // take work items blockIdx.x, + gridDim.x, ... (gridDim.x a multiple of 8 keeps every item on
-// its XCD). The workgroups of every other block of 128 copy each chunk one item late: they
+// its XCD). Half of the workgroups (which half: below) copy each chunk one item late: they
 // resolve the next chunk first, holding the previous chunk's indices in four registers per
 // thread. Launched all at once, workgroups that each resolve and then copy stay in step,
 // round after round: the whole chip resolves (HBM idle), and then it copies. With half of
@@ -118,12 +118,13 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(ResolveArgs a) {
 // layer (B4 H64 T16384, d_v 24): 104.1 and 91.0 us.
 // Which half lags (`mode` bit 1): workgroups are dealt to the 8 XCDs in turn, and where each
 // XCD spreads its share over its 32 CUs in order, a block of 128 takes one slot on half of
-// every XCD's CUs, so lagging every other block (bid >> 7 odd) makes whole CUs lag, and every
-// other block of 256 (bid >> 8 odd) lags two of each CU's four workgroups instead. Long value rows favour the second (B8 H16 T16384 Zipf codes,
-// d_v 64: 79.8-80.8 against 81.2-81.3 us back to back, 100.9-101.4 against 104.9-105.0 us
-// after a cache eviction; with y interleaved 117.5 against 120.3 us and 107.5 against 112),
-// short ones the first (language-model layer, d_v 24, y interleaved: 91.8-92.1 against
-// 94.1-94.3 us at B4; after an eviction 63.5 against 66.3 us at B2).
+// every XCD's CUs. Lagging every other block of 128 (bid >> 7 odd) then makes whole CUs lag;
+// lagging every other block of 256 (bid >> 8 even: slots 0 and 2) lags two of each CU's four
+// workgroups instead. Long value rows favour the second (B8 H16 T16384 Zipf codes, d_v 64:
+// 78.8-79.2 against 81.2-81.3 us back to back, 100.8 against 104.9-105.0 us after a cache
+// eviction; slots 1 and 3 instead: 79.5-81.4 and 100.9-101.7 us), short ones the first
+// (language-model layer, d_v 24, y interleaved: 91.8-92.1 against 94.1-94.3 us at B4; after
+// an eviction 63.5 against 66.3 us at B2).
 // `mode` bit 0 asks item_of for alternating chunk order.
 template <typename CodeT, int VEC, bool kSumm>
 __global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_lag_kernel(ResolveArgs a, int32_t items,
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(kThreads, sizeof(CodeT) == 4 ? 4 : 3) void resolve_
   static_assert(VEC > 0, "the persistent form exists for copies");
   __shared__ ResolveLds<CodeT> s;
   const int bid = blockIdx.x, G = gridDim.x;
-  const bool lagged = (mode & 2) ? (bid >> 8) & 1 : (bid >> 7) & 1;
+  const bool lagged = (mode & 2) ? !((bid >> 8) & 1) : (bid >> 7) & 1;
   auto bar = [] { __syncthreads(); };
   int32_t* srcs = reinterpret_cast<int32_t*>(s.mbits);  // the masks are dead while copying
   const int n = bid < items ? (items - bid + G - 1) / G : 0;
