@@ -282,8 +282,8 @@ extern "C" int lema_qk_pack_bf16(const void* x, int64_t ldx, const void* wq, con
                d <= 32 ? 4 : 8);
   LEMA_REQUIRE(T > 0 && M % T == 0, "rows %lld must be whole streams of %lld", (long long)M,
                (long long)T);
-  LEMA_REQUIRE(M / d * N * code_bytes < (int64_t(1) << 31), "codes of %lld bytes: at most 2 GiB",
-               (long long)(M / d * N * code_bytes));
+  LEMA_REQUIRE(M * (N / d) * code_bytes < (int64_t(1) << 31), "codes of %lld bytes: at most 2 GiB",
+               (long long)(M * (N / d) * code_bytes));
   LEMA_REQUIRE(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 && ldx < (1 << 20) &&
                    ldw < (1 << 20),
                "row strides must be >= K and multiples of 8");

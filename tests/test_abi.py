@@ -53,6 +53,17 @@ def test_host_validation_statuses(L):
     assert b"at most 2048" in L.lema_last_error()
     assert f(256, 512, 768, 1e-5, 1024, 1280, 1536, 2048, 32, 64, 2048, 1792, None) == _lib.BAD_ARG
     assert b"LDS" in L.lema_last_error()
+    # prefill q/k codes: x, ldx, wq, wk, ldw, M, N, K, d, T, qcodes, kcodes, code_bytes, stream
+    # (null pointers: the shape is refused before any pointer is looked at);
+    # M rows x N / d heads x 4 bytes = 2^31 bytes of codes per projection, one past the limit
+    # (M is not a multiple of d here, so the size is M * (N / d), not M / d * N)
+    q = L.lema_qk_pack_bf16
+    assert q(None, 1536, None, None, 1536, 8388608, 1536, 1536, 24, 16384, None, None, 4,
+             None) == _lib.BAD_ARG
+    assert b"2 GiB" in L.lema_last_error()
+    assert q(None, 1536, None, None, 1536, 8386560, 1536, 1536, 24, 16384, None, None, 4,
+             None) == _lib.BAD_ARG
+    assert b"whole streams" in L.lema_last_error()  # the size passes; T does not divide M
     assert L.lema_argmax_bf16(256, 2, 7, 8, 512, 1, None) == _lib.BAD_ARG
     assert L.lema_embedding_bf16(256, 10, 12, 512, 3, 768, None) == _lib.BAD_ARG
     # empty work is a no-op that touches no pointer
