@@ -226,8 +226,9 @@ int lema_skinny_qkv_bf16(const void* x, int64_t ldx, const void* wq, const void*
  * [N, K] bf16, row strides ldx, ldw), bit j of a head's code = (bf16(z_j) >= 0), z never
  * stored. A persistent MFMA GEMM with the sign-pack in its epilogue. Replaces project +
  * pack_codes (code/lema/model.py:168-175, code/lema/attention.py:82-97) on prefill shapes:
- * M a multiple of 2048, N a multiple of 256 up to 65536, K of 64, d a multiple of 8 up to 64,
- * code_bytes 4 for d <= 32 and 8 above, at most 2 GiB of codes. */
+ * M a multiple of 2048, N a multiple of 256 up to 65536, K a multiple of 64, d a multiple of
+ * 8 up to 64, code_bytes 4 for d <= 32 and 8 above, under 2 GiB of codes per projection
+ * (M * N / d * code_bytes < 2^31). */
 int lema_qk_pack_bf16(const void* x, int64_t ldx, const void* wq, const void* wk, int64_t ldw,
                       int64_t M, int64_t N, int64_t K, int32_t d, int64_t T, void* qcodes,
                       void* kcodes, int32_t code_bytes, void* stream);
